@@ -1,0 +1,212 @@
+/*
+ * nerve_sampler.h -- C ABI of the MI355X (gfx950) token-sampling stage.
+ *
+ * One fused HIP launch samples every row of a decode batch: allowed-token
+ * mask, repetition / frequency / presence penalties, temperature, top-k,
+ * min-p, top-p and an argmax or seeded multinomial draw. Plain C types only;
+ * device pointers are HIP device addresses owned by the caller, the library
+ * owns only its scratch. Everything is asynchronous on the stream passed in.
+ * Calls on one handle are not thread-safe; distinct handles may be used
+ * concurrently (each owns its scratch).
+ *
+ * Reference surface each entry point replaces (paths under the reference root,
+ * runtime-rs/src/vulkan_stream_circuit/):
+ *   nerve_sampler_spec / nerve_sampler_runtime_config  <- VulkanResidentSamplerSpec
+ *        and VulkanResidentSamplerRuntimeConfig (sampler.rs:29-54)
+ *   nerve_sampler_apply_runtime_config                 <- RuntimeConfig::apply_to (sampler.rs:66-141)
+ *   nerve_sampler_validate_spec                        <- spec checks in
+ *        from_logits_buffer_with_feedback_control (sampler.rs:259-382)
+ *   nerve_sampler_kernel_role_matches                  <- sampler_kernel_role_matches (sampler.rs:144-160)
+ *   nerve_sampler_create / nerve_sampler_destroy       <- VulkanResidentSamplerRunner construction / Drop
+ *        (sampler.rs:245-727), batched over B lanes
+ *   nerve_sampler_step                                 <- VulkanResidentBatchedOutputProjectionRunner::sample_lanes
+ *        (batched_output_projection.rs:316-371) and VulkanResidentSamplerRunner::run (sampler.rs:748-759):
+ *        one launch for all rows instead of B two-dispatch sequences
+ *   nerve_sampler_record_tokens                        <- record_input_tokens (sampler.rs:773-814) and
+ *        VulkanResidentSamplerLogitsView::prepare_token_state (sampler.rs:1146-1193)
+ *   nerve_sampler_copy_token_state                     <- capture_token_state / restore_token_state
+ *        (sampler.rs:816-828)
+ *   nerve_sampler_output / stream-control ring         <- VulkanResidentSamplerRun (sampler.rs:1221-1230),
+ *        completed_run_at (sampler.rs:852-873), output record of greedy_sampler_f32.comp.template:85-107
+ *   nerve_status codes                                 <- VulkanResidentSamplerRunnerError (sampler.rs:1232-1258)
+ */
+#ifndef NERVE_SAMPLER_H
+#define NERVE_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NERVE_SAMPLER_ABI_VERSION 1u
+
+typedef enum {
+    NERVE_OK = 0,
+    NERVE_ERR_INVALID_LOGITS_BYTE_CAPACITY = 1,
+    NERVE_ERR_ZERO_HISTORY_CAPACITY = 2,
+    NERVE_ERR_HISTORY_CAPACITY_OVERFLOW = 3,
+    NERVE_ERR_TOKEN_BATCH_CAPACITY_EXCEEDED = 4,
+    NERVE_ERR_INVALID_KERNEL_ROLE = 5,
+    NERVE_ERR_UNSUPPORTED_RUNTIME_SAMPLING_OVERRIDE = 6,
+    NERVE_ERR_INVALID_SAMPLING_SPEC = 7,
+    NERVE_ERR_HIP = 8,
+    NERVE_ERR_INVALID_ARGUMENT = 9,
+    NERVE_ERR_BATCH_CAPACITY_EXCEEDED = 10
+} nerve_status;
+
+enum { NERVE_DTYPE_F32 = 0, NERVE_DTYPE_BF16 = 1 };
+enum { NERVE_METHOD_GREEDY = 0, NERVE_METHOD_TEMPERATURE_TOP_K_TOP_P = 1 };
+enum { NERVE_RNG_REFERENCE_HASH = 0, NERVE_RNG_PHILOX = 1 };
+enum { NERVE_FLAG_SAMPLED = 1u, NERVE_FLAG_EOS_FALLBACK = 2u };
+
+/* Up to this many token ids per row per record call
+ * (VULKAN_BACKEND_LOOP_MAX_WINDOW, vulkan_stream_circuit.rs:82). */
+#define NERVE_TOKEN_BATCH_CAPACITY 64u
+#define NERVE_MAX_TOP_K_CAPACITY 1024u
+#define NERVE_MAX_HISTORY_CAPACITY 4095u
+#define NERVE_MAX_VOCAB 1048575u
+
+/* ---- Host-side spec surface (no device work) ---------------------------- */
+
+#define NERVE_SAMPLER_ID_CAPACITY 64
+
+typedef struct {
+    char sampler_id[NERVE_SAMPLER_ID_CAPACITY];
+    uint32_t method; /* NERVE_METHOD_* */
+    float temperature;
+    uint32_t top_k;
+    float top_p;
+    float min_p;
+    float presence_penalty;
+    float repetition_penalty;
+    uint32_t top_k_capacity;
+    uint32_t runtime_parameterized;
+    uint64_t logits_byte_capacity;
+    uint64_t output_byte_capacity;
+    uint64_t scratch_byte_capacity;
+} nerve_sampler_spec;
+
+/* Each field applies only when its has_* flag is nonzero (Rust Option<_>). */
+typedef struct {
+    uint32_t has_temperature, has_top_k, has_top_p, has_min_p, has_presence_penalty, has_repetition_penalty;
+    float temperature;
+    uint32_t top_k;
+    float top_p;
+    float min_p;
+    float presence_penalty;
+    float repetition_penalty;
+} nerve_sampler_runtime_config;
+
+/* Greedy -> sampled promotion and validation; writes `out` on success.
+ * On failure returns NERVE_ERR_UNSUPPORTED_RUNTIME_SAMPLING_OVERRIDE and, if
+ * `message` is non-null, the reason (contains "capacity <n>"). */
+int nerve_sampler_apply_runtime_config(const nerve_sampler_spec *compiled,
+                                       const nerve_sampler_runtime_config *config,
+                                       nerve_sampler_spec *out, char *message, size_t message_capacity);
+
+/* Spec checks at runner construction; vocab_size = logits_byte_capacity / 4. */
+int nerve_sampler_validate_spec(const nerve_sampler_spec *spec, uint64_t logits_byte_capacity,
+                                uint32_t history_capacity_activations, uint32_t partition_count);
+
+/* Kernel-role table of the reference; kept for callers that select roles. */
+int nerve_sampler_kernel_role_matches(const char *role, uint32_t runtime_parameterized, uint32_t method);
+
+/* ---- Device sampler ----------------------------------------------------- */
+
+typedef struct nerve_sampler nerve_sampler;
+
+typedef struct {
+    uint32_t vocab_size;        /* V, 1..NERVE_MAX_VOCAB */
+    uint32_t max_batch;         /* rows per step */
+    uint32_t dtype;             /* NERVE_DTYPE_* of the logits */
+    uint32_t top_k_capacity;    /* 1..NERVE_MAX_TOP_K_CAPACITY */
+    uint32_t history_capacity;  /* max history ids per row, 0..NERVE_MAX_HISTORY_CAPACITY */
+    uint32_t slices_per_row;    /* 0 = automatic; workgroups cooperating on one row */
+    uint32_t device;            /* HIP device ordinal */
+    uint32_t reserved;
+} nerve_sampler_desc;
+
+/* Per-row sampling parameters (device array [batch], 32 bytes each). */
+typedef struct {
+    uint32_t method;            /* NERVE_METHOD_* */
+    float temperature;          /* > 0 */
+    uint32_t top_k;             /* 1..top_k_capacity (clamped on device) */
+    float top_p;                /* (0, 1] */
+    float min_p;                /* [0, 1] */
+    float repetition_penalty;   /* > 0 */
+    float frequency_penalty;    /* finite; subtracts penalty * count */
+    float presence_penalty;     /* finite */
+} nerve_sampler_row_params;
+
+/* Output record: words 0-3 of the reference sampler output buffer. */
+typedef struct {
+    uint32_t token_id;
+    uint32_t selected_logit_bits; /* penalised, pre-temperature logit */
+    uint32_t flags;               /* NERVE_FLAG_* */
+    uint32_t reserved;
+} nerve_sampler_output;
+
+typedef struct {
+    uint32_t batch;                        /* rows this step, <= max_batch */
+    uint32_t rng;                          /* NERVE_RNG_* */
+    const void *logits;                    /* [batch][logits_row_stride] of dtype */
+    uint64_t logits_row_stride;            /* elements, >= vocab_size */
+    const nerve_sampler_row_params *params;/* [batch] */
+    /* Penalty state, at most one of: */
+    const uint32_t *history;               /* [batch][history_stride] token ids (count semantics) */
+    const uint32_t *history_len;           /* [batch] valid ids per row */
+    uint32_t history_stride;               /* <= history_capacity */
+    const uint32_t *seen;                  /* [batch][seen_stride] packed bitmap (set semantics) */
+    uint32_t seen_stride;                  /* words, >= ceil(V/32) */
+    /* Allowed-token bitmask (optional); an all-zero row samples eos_token_id. */
+    const uint32_t *allowed;               /* [batch][allowed_stride] */
+    uint32_t allowed_stride;
+    uint32_t eos_token_id;
+    /* Draw key: seeds[row] and the stream tick (from stream_control when set, else steps[row]). */
+    const uint32_t *seeds;                 /* [batch] */
+    const uint64_t *steps;                 /* [batch] */
+    /* Optional reference stream control: [batch][5] words {token, tick_lo, tick_hi, flags,
+     * history_capacity}; the step writes the token and advances the 64-bit tick. */
+    uint32_t *stream_control;
+    /* Optional reference output ring: [batch][ring_stride] words; record at words 0-3 and at
+     * 4 + (tick_lo % history_capacity) * 4. Requires stream_control. */
+    uint32_t *output_ring;
+    uint32_t ring_stride;
+    nerve_sampler_output *out;             /* [batch] (required) */
+    /* Optional survivors: [batch][top_k_capacity]; padding id 0xffffffff, logit -FLT_MAX, prob 0. */
+    uint32_t *topk_ids;
+    float *topk_logits;
+    float *topk_probs;
+} nerve_sampler_batch;
+
+int nerve_sampler_create(const nerve_sampler_desc *desc, nerve_sampler **out);
+int nerve_sampler_destroy(nerve_sampler *sampler);
+
+/* One decode step for every row of `batch`, asynchronous on `stream`
+ * (a hipStream_t; NULL = the device's null stream). */
+int nerve_sampler_step(nerve_sampler *sampler, const nerve_sampler_batch *batch, void *stream);
+
+/* Sets bits for token ids < vocab_size into per-row seen bitmaps:
+ * seen[row*seen_stride + id/32] |= 1 << (id%32) for ids[row*ids_stride + i], i < min(counts[row], max_count).
+ * ids and counts are device arrays; max_count is the host-side bound of the call and must be
+ * 1..NERVE_TOKEN_BATCH_CAPACITY (else NERVE_ERR_TOKEN_BATCH_CAPACITY_EXCEEDED), like the reference. */
+int nerve_sampler_record_tokens(nerve_sampler *sampler, uint32_t *seen, uint32_t seen_stride, uint32_t rows,
+                                const uint32_t *ids, uint32_t ids_stride, const uint32_t *counts,
+                                uint32_t max_count, void *stream);
+
+/* Device-to-device copy of `rows` seen bitmaps (capture: live -> snapshot; restore: snapshot -> live). */
+int nerve_sampler_copy_token_state(nerve_sampler *sampler, uint32_t *dst, const uint32_t *src, uint32_t rows,
+                                   uint32_t seen_stride, void *stream);
+
+/* Last HIP error text for this thread, or "" */
+const char *nerve_sampler_last_error(void);
+uint32_t nerve_sampler_abi_version(void);
+/* Workgroups per row that the next step of this handle will use. */
+uint32_t nerve_sampler_slices_per_row(const nerve_sampler *sampler);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

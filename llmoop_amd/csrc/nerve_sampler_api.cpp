@@ -1,0 +1,385 @@
+// nerve_sampler_api.cpp -- host side of the C ABI declared in include/nerve_sampler.h.
+//
+// Spec and runtime-override logic restate the reference's Rust runner
+// (runtime-rs/src/vulkan_stream_circuit/sampler.rs); the device handle owns
+// only the cross-workgroup scratch of the fused kernel. Every failure is
+// reported as a status code; nothing falls back to a CPU path.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "nerve_sampler.h"
+#include "nerve_sampler_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int hip_fail(hipError_t e, const char *what) {
+    g_last_error = std::string(what) + ": " + hipGetErrorString(e);
+    return NERVE_ERR_HIP;
+}
+
+int fail(int code, const std::string &msg) {
+    g_last_error = msg;
+    return code;
+}
+
+bool is_finite(float v) { return std::isfinite(v); }
+
+const char *method_name(uint32_t m) {
+    return m == NERVE_METHOD_GREEDY ? "greedy"
+           : m == NERVE_METHOD_TEMPERATURE_TOP_K_TOP_P ? "temperature_top_k_top_p"
+                                                        : "unknown";
+}
+
+uint32_t next_pow2(uint32_t v) {
+    uint32_t p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+
+uint32_t log2u(uint32_t v) {
+    uint32_t l = 0;
+    while ((1u << l) < v) ++l;
+    return l;
+}
+
+}  // namespace
+
+struct nerve_sampler {
+    nerve_sampler_desc desc;
+    int device;
+    uint32_t slices;           // requested workgroups per row (raised per step if the slice would not fit)
+    uint32_t slices_capacity;  // scratch sized for this many
+    uint2 *scratch_lists;
+    uint32_t *scratch_meta;
+    uint32_t *counters;
+    size_t lds_per_block;      // hipDeviceProp_t::sharedMemPerBlock
+};
+
+extern "C" {
+
+uint32_t nerve_sampler_abi_version(void) { return NERVE_SAMPLER_ABI_VERSION; }
+
+const char *nerve_sampler_last_error(void) { return g_last_error.c_str(); }
+
+// sampler.rs:144-160
+int nerve_sampler_kernel_role_matches(const char *role, uint32_t runtime_parameterized, uint32_t method) {
+    if (!role) return 0;
+    const std::string r(role);
+    if (method == NERVE_METHOD_GREEDY) return runtime_parameterized ? r == "runtime_sample_logits" : r == "sample_logits";
+    if (method == NERVE_METHOD_TEMPERATURE_TOP_K_TOP_P) {
+        if (runtime_parameterized) return r == "runtime_partition_top_k" || r == "runtime_sample_candidates";
+        return r == "partition_top_k" || r == "sample_candidates";
+    }
+    return 0;
+}
+
+// sampler.rs:66-141
+int nerve_sampler_apply_runtime_config(const nerve_sampler_spec *compiled, const nerve_sampler_runtime_config *cfg,
+                                       nerve_sampler_spec *out, char *message, size_t message_capacity) {
+    if (!compiled || !cfg || !out) return fail(NERVE_ERR_INVALID_ARGUMENT, "null argument");
+    const bool empty = !cfg->has_temperature && !cfg->has_top_k && !cfg->has_top_p && !cfg->has_min_p &&
+                       !cfg->has_presence_penalty && !cfg->has_repetition_penalty;
+    if (empty) {
+        *out = *compiled;
+        return NERVE_OK;
+    }
+    nerve_sampler_spec e = *compiled;
+    const bool sampled_request = cfg->has_temperature || cfg->has_top_k || cfg->has_top_p || cfg->has_min_p;
+    if (compiled->method == NERVE_METHOD_GREEDY && sampled_request) {
+        std::snprintf(e.sampler_id, sizeof(e.sampler_id), "%s", "runtime_temperature_top_k_top_p_sampler");
+        e.method = NERVE_METHOD_TEMPERATURE_TOP_K_TOP_P;
+        e.temperature = 1.0f;
+        e.top_k = e.top_k_capacity < 50u ? e.top_k_capacity : 50u;
+        e.top_p = 1.0f;
+        e.min_p = 0.0f;
+    }
+    if (cfg->has_temperature) e.temperature = cfg->temperature;
+    if (cfg->has_top_k) e.top_k = cfg->top_k;
+    if (cfg->has_top_p) e.top_p = cfg->top_p;
+    if (cfg->has_min_p) e.min_p = cfg->min_p;
+    if (cfg->has_presence_penalty) e.presence_penalty = cfg->presence_penalty;
+    if (cfg->has_repetition_penalty) e.repetition_penalty = cfg->repetition_penalty;
+    const bool valid_common =
+        is_finite(e.presence_penalty) && is_finite(e.repetition_penalty) && e.repetition_penalty > 0.0f;
+    bool valid = false;
+    if (e.method == NERVE_METHOD_GREEDY) {
+        valid = e.min_p == 0.0f && valid_common;
+    } else if (e.method == NERVE_METHOD_TEMPERATURE_TOP_K_TOP_P) {
+        valid = is_finite(e.temperature) && e.temperature > 0.0f && e.top_k > 0u && e.top_k <= e.top_k_capacity &&
+                is_finite(e.top_p) && e.top_p > 0.0f && e.top_p <= 1.0f && is_finite(e.min_p) && e.min_p >= 0.0f &&
+                e.min_p <= 1.0f && valid_common;
+    }
+    if (!valid) {
+        char buf[512];
+        std::snprintf(buf, sizeof(buf),
+                      "runtime sampler override is invalid for method \"%s\": temperature=%g, top_k=%u (capacity %u), "
+                      "top_p=%g, min_p=%g, presence_penalty=%g, repetition_penalty=%g",
+                      method_name(e.method), (double)e.temperature, e.top_k, e.top_k_capacity, (double)e.top_p,
+                      (double)e.min_p, (double)e.presence_penalty, (double)e.repetition_penalty);
+        if (message && message_capacity) std::snprintf(message, message_capacity, "%s", buf);
+        return fail(NERVE_ERR_UNSUPPORTED_RUNTIME_SAMPLING_OVERRIDE, buf);
+    }
+    e.runtime_parameterized = 1u;
+    *out = e;
+    return NERVE_OK;
+}
+
+// Construction-time checks of sampler.rs:259-382 that do not concern SPIR-V
+// kernel artifacts: logits capacity, history capacity, method parameters and
+// the partition scratch size (G * k * 8 bytes).
+int nerve_sampler_validate_spec(const nerve_sampler_spec *s, uint64_t logits_byte_capacity,
+                                uint32_t history_capacity_activations, uint32_t partition_count) {
+    if (!s) return fail(NERVE_ERR_INVALID_ARGUMENT, "null spec");
+    if (logits_byte_capacity != s->logits_byte_capacity) {
+        char buf[160];
+        std::snprintf(buf, sizeof(buf), "sampler logits buffer has %llu bytes, expected %llu",
+                      (unsigned long long)logits_byte_capacity, (unsigned long long)s->logits_byte_capacity);
+        return fail(NERVE_ERR_INVALID_LOGITS_BYTE_CAPACITY, buf);
+    }
+    if (history_capacity_activations == 0u) return fail(NERVE_ERR_ZERO_HISTORY_CAPACITY, "sampler history capacity must be nonzero");
+    const uint64_t vocab = logits_byte_capacity / 4u;
+    const uint32_t per_partition = s->runtime_parameterized ? s->top_k_capacity : s->top_k;
+    bool ok = false;
+    if (s->method == NERVE_METHOD_GREEDY) {
+        ok = s->min_p == 0.0f && is_finite(s->presence_penalty) && is_finite(s->repetition_penalty) &&
+             s->repetition_penalty > 0.0f;
+    } else if (s->method == NERVE_METHOD_TEMPERATURE_TOP_K_TOP_P) {
+        const uint64_t required = (uint64_t)partition_count * per_partition * 8u;
+        ok = is_finite(s->temperature) && s->temperature > 0.0f && s->top_k > 0u && s->top_k <= vocab &&
+             is_finite(s->top_p) && s->top_p > 0.0f && s->top_p <= 1.0f && is_finite(s->min_p) && s->min_p >= 0.0f &&
+             s->min_p <= 1.0f && is_finite(s->presence_penalty) && is_finite(s->repetition_penalty) &&
+             s->repetition_penalty > 0.0f && s->top_k <= s->top_k_capacity && partition_count > 0u &&
+             required <= s->scratch_byte_capacity;
+    }
+    if (!ok) {
+        char buf[320];
+        std::snprintf(buf, sizeof(buf),
+                      "invalid resident sampling spec method=\"%s\" temperature=%g top_k=%u top_p=%g min_p=%g "
+                      "presence_penalty=%g repetition_penalty=%g",
+                      method_name(s->method), (double)s->temperature, s->top_k, (double)s->top_p, (double)s->min_p,
+                      (double)s->presence_penalty, (double)s->repetition_penalty);
+        return fail(NERVE_ERR_INVALID_SAMPLING_SPEC, buf);
+    }
+    const uint64_t history_bytes = (uint64_t)history_capacity_activations * 16u + s->output_byte_capacity;
+    if (history_bytes < s->output_byte_capacity) return fail(NERVE_ERR_HISTORY_CAPACITY_OVERFLOW, "sampler history byte capacity overflowed");
+    return NERVE_OK;
+}
+
+int nerve_sampler_create(const nerve_sampler_desc *desc, nerve_sampler **out) {
+    if (!desc || !out) return fail(NERVE_ERR_INVALID_ARGUMENT, "null argument");
+    *out = nullptr;
+    const nerve_sampler_desc d = *desc;
+    if (d.vocab_size == 0u || d.vocab_size > NERVE_MAX_VOCAB)
+        return fail(NERVE_ERR_INVALID_ARGUMENT, "vocab_size must be in 1..1048575");
+    if (d.max_batch == 0u) return fail(NERVE_ERR_INVALID_ARGUMENT, "max_batch must be nonzero");
+    if (d.dtype != NERVE_DTYPE_F32 && d.dtype != NERVE_DTYPE_BF16) return fail(NERVE_ERR_INVALID_ARGUMENT, "dtype must be f32 or bf16");
+    if (d.top_k_capacity == 0u || d.top_k_capacity > NERVE_MAX_TOP_K_CAPACITY)
+        return fail(NERVE_ERR_INVALID_SAMPLING_SPEC, "top_k_capacity must be in 1..1024");
+    if (d.history_capacity > NERVE_MAX_HISTORY_CAPACITY)
+        return fail(NERVE_ERR_HISTORY_CAPACITY_OVERFLOW, "history_capacity must be <= 4095");
+    int ndev = 0;
+    hipError_t e = hipGetDeviceCount(&ndev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    if ((int)d.device >= ndev) return fail(NERVE_ERR_INVALID_ARGUMENT, "device ordinal out of range");
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, (int)d.device);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(NERVE_ERR_HIP, std::string("the sampler kernels are built for gfx950 only, device is ") + prop.gcnArchName);
+
+    // Slices per row: enough that one workgroup's share of the row fits its
+    // registers (checked again per step for the variant the alignment picks),
+    // and more when the batch is small so the launch still covers the CUs.
+    const uint32_t threads = nerve::block_threads();
+    const uint32_t scalar_tokens_per_wg = threads * nerve::elems_per_thread(nerve::kVariantF32Scalar);
+    const uint32_t slices_worst = (d.vocab_size + scalar_tokens_per_wg - 1u) / scalar_tokens_per_wg;
+    uint32_t want = d.slices_per_row;
+    if (want == 0u) {
+        const uint32_t cus = (uint32_t)prop.multiProcessorCount;
+        want = (2u * cus + d.max_batch - 1u) / d.max_batch;
+        const uint32_t by_size = d.vocab_size / (threads * 4u);  // keep >= ~4 elements per lane
+        if (want > by_size) want = by_size;
+        if (want > 64u) want = 64u;
+        const uint32_t by_merge = 12288u / d.top_k_capacity;  // merge area of the last workgroup
+        if (want > by_merge) want = by_merge;
+        if (want == 0u) want = 1u;
+    }
+    const uint32_t capacity = want > slices_worst ? want : slices_worst;
+    if ((uint64_t)capacity * d.top_k_capacity > 12288u)
+        return fail(NERVE_ERR_INVALID_SAMPLING_SPEC, "slices_per_row * top_k_capacity exceeds the 12288-entry merge area");
+
+    nerve_sampler *s = new (std::nothrow) nerve_sampler();
+    if (!s) return fail(NERVE_ERR_INVALID_ARGUMENT, "out of host memory");
+    s->desc = d;
+    s->device = (int)d.device;
+    s->slices = want;
+    s->slices_capacity = capacity;
+    s->lds_per_block = prop.sharedMemPerBlock;
+    int prev = 0;
+    hipGetDevice(&prev);
+    hipSetDevice(s->device);
+    const size_t lists_bytes = (size_t)d.max_batch * capacity * d.top_k_capacity * sizeof(uint2);
+    const size_t meta_bytes = (size_t)d.max_batch * capacity * sizeof(uint32_t);
+    const size_t counter_bytes = (size_t)d.max_batch * sizeof(uint32_t);
+    e = hipMalloc((void **)&s->scratch_lists, lists_bytes);
+    if (e == hipSuccess) e = hipMalloc((void **)&s->scratch_meta, meta_bytes);
+    if (e == hipSuccess) e = hipMalloc((void **)&s->counters, counter_bytes);
+    if (e == hipSuccess) e = hipMemset(s->counters, 0, counter_bytes);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    hipSetDevice(prev);
+    if (e != hipSuccess) {
+        int rc = hip_fail(e, "nerve_sampler_create scratch");
+        nerve_sampler_destroy(s);
+        return rc;
+    }
+    *out = s;
+    return NERVE_OK;
+}
+
+int nerve_sampler_destroy(nerve_sampler *s) {
+    if (!s) return NERVE_OK;
+    int prev = 0;
+    hipGetDevice(&prev);
+    hipSetDevice(s->device);
+    if (s->scratch_lists) hipFree(s->scratch_lists);
+    if (s->scratch_meta) hipFree(s->scratch_meta);
+    if (s->counters) hipFree(s->counters);
+    hipSetDevice(prev);
+    delete s;
+    return NERVE_OK;
+}
+
+uint32_t nerve_sampler_slices_per_row(const nerve_sampler *s) { return s ? s->slices : 0u; }
+
+int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *stream) {
+    if (!s || !b) return fail(NERVE_ERR_INVALID_ARGUMENT, "null argument");
+    const nerve_sampler_desc &d = s->desc;
+    if (b->batch == 0u) return NERVE_OK;
+    if (b->batch > d.max_batch) return fail(NERVE_ERR_BATCH_CAPACITY_EXCEEDED, "batch exceeds max_batch");
+    if (!b->logits || !b->params || !b->out) return fail(NERVE_ERR_INVALID_ARGUMENT, "logits, params and out are required");
+    if (b->logits_row_stride < d.vocab_size) return fail(NERVE_ERR_INVALID_LOGITS_BYTE_CAPACITY, "logits_row_stride < vocab_size");
+    if (b->rng != NERVE_RNG_REFERENCE_HASH && b->rng != NERVE_RNG_PHILOX) return fail(NERVE_ERR_INVALID_ARGUMENT, "unknown rng");
+    if (b->history && b->seen) return fail(NERVE_ERR_INVALID_ARGUMENT, "pass a history list or a seen bitmap, not both");
+    const uint32_t words = (d.vocab_size + 31u) / 32u;
+    if (b->history) {
+        if (!b->history_len) return fail(NERVE_ERR_INVALID_ARGUMENT, "history_len is required with history");
+        if (b->history_stride == 0u || b->history_stride > d.history_capacity)
+            return fail(NERVE_ERR_HISTORY_CAPACITY_OVERFLOW, "history_stride must be in 1..history_capacity");
+    }
+    if (b->seen && b->seen_stride < words) return fail(NERVE_ERR_INVALID_ARGUMENT, "seen_stride < ceil(vocab/32)");
+    if (b->allowed && b->allowed_stride < words) return fail(NERVE_ERR_INVALID_ARGUMENT, "allowed_stride < ceil(vocab/32)");
+    if (b->output_ring && !b->stream_control) return fail(NERVE_ERR_INVALID_ARGUMENT, "output_ring requires stream_control");
+    if (b->output_ring && b->ring_stride < 4u) return fail(NERVE_ERR_INVALID_ARGUMENT, "ring_stride must hold the 4-word record");
+
+    const size_t esize = d.dtype == NERVE_DTYPE_F32 ? 4u : 2u;
+    const bool aligned = ((uintptr_t)b->logits % 16u == 0u) && ((b->logits_row_stride * esize) % 16u == 0u);
+    uint32_t variant;
+    if (d.dtype == NERVE_DTYPE_F32) variant = aligned ? nerve::kVariantF32Vec : nerve::kVariantF32Scalar;
+    else variant = aligned ? nerve::kVariantBf16Vec : nerve::kVariantBf16Scalar;
+
+    const uint32_t epv = nerve::elems_per_vector(variant);
+    const uint32_t per_thread = nerve::elems_per_thread(variant);
+    const uint32_t threads = nerve::block_threads();
+    const uint32_t nvec = (d.vocab_size + epv - 1u) / epv;
+    const uint32_t vec_budget = threads * (per_thread / epv);
+    uint32_t slices = s->slices;
+    const uint32_t slices_min = (nvec + vec_budget - 1u) / vec_budget;
+    if (slices < slices_min) slices = slices_min;
+    if (slices > s->slices_capacity) return fail(NERVE_ERR_INVALID_ARGUMENT, "slice count exceeds the scratch capacity");
+    const uint32_t vec_per_slice = (nvec + slices - 1u) / slices;
+    if (vec_per_slice > vec_budget) return fail(NERVE_ERR_INVALID_ARGUMENT, "slice exceeds one workgroup's register budget");
+
+    nerve::StepArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.logits = b->logits;
+    a.ld = b->logits_row_stride;
+    a.params = b->params;
+    a.history = b->history;
+    a.history_len = b->history_len;
+    a.history_stride = b->history ? b->history_stride : 0u;
+    a.seen = b->seen;
+    a.seen_stride = b->seen_stride;
+    a.allowed = b->allowed;
+    a.allowed_stride = b->allowed_stride;
+    a.seeds = b->seeds;
+    a.steps = b->steps;
+    a.stream_control = b->stream_control;
+    a.ring = b->output_ring;
+    a.ring_stride = b->ring_stride;
+    a.out = b->out;
+    a.topk_ids = b->topk_ids;
+    a.topk_logits = b->topk_logits;
+    a.topk_probs = b->topk_probs;
+    a.scratch_lists = s->scratch_lists;
+    a.scratch_meta = s->scratch_meta;
+    a.counters = s->counters;
+    a.vocab = d.vocab_size;
+    a.batch = b->batch;
+    a.slices = slices;
+    a.kcap = d.top_k_capacity;
+    a.rng = b->rng;
+    a.eos = b->eos_token_id;
+    a.nvec = nvec;
+    a.vec_per_slice = vec_per_slice;
+    if (b->history) {
+        a.hash_slots = next_pow2(2u * b->history_stride);
+        if (a.hash_slots < 64u) a.hash_slots = 64u;
+        a.log2_slots = log2u(a.hash_slots);
+    }
+    uint32_t big = nerve::cand_capacity();
+    if (slices * d.top_k_capacity > big) big = slices * d.top_k_capacity;
+    a.big_entries = big;
+    a.dyn_lds_bytes = a.hash_slots * 4u + big * 8u + d.top_k_capacity * 8u;
+    const size_t static_lds = 8u * 1024u;  // slice bitmap (<= 4 KiB) and reduction scratch
+    if (a.dyn_lds_bytes + static_lds > s->lds_per_block)
+        return fail(NERVE_ERR_INVALID_ARGUMENT, "LDS need of this top_k_capacity / history / slice count exceeds the device");
+
+    int prev = 0;
+    hipGetDevice(&prev);
+    if (prev != s->device) hipSetDevice(s->device);
+    hipError_t e = nerve::launch_sample_rows(variant, a, (hipStream_t)stream);
+    if (prev != s->device) hipSetDevice(prev);
+    if (e != hipSuccess) return hip_fail(e, "sample_rows launch");
+    return NERVE_OK;
+}
+
+int nerve_sampler_record_tokens(nerve_sampler *s, uint32_t *seen, uint32_t seen_stride, uint32_t rows,
+                                const uint32_t *ids, uint32_t ids_stride, const uint32_t *counts, uint32_t max_count,
+                                void *stream) {
+    if (!s || !seen || !ids || !counts) return fail(NERVE_ERR_INVALID_ARGUMENT, "null argument");
+    if (max_count == 0u || max_count > NERVE_TOKEN_BATCH_CAPACITY) {
+        char buf[128];
+        std::snprintf(buf, sizeof(buf), "sampler repetition-state batch requests %u tokens, capacity is %u", max_count,
+                      NERVE_TOKEN_BATCH_CAPACITY);
+        return fail(NERVE_ERR_TOKEN_BATCH_CAPACITY_EXCEEDED, buf);
+    }
+    if (rows == 0u) return NERVE_OK;
+    if (seen_stride < (s->desc.vocab_size + 31u) / 32u) return fail(NERVE_ERR_INVALID_ARGUMENT, "seen_stride < ceil(vocab/32)");
+    int prev = 0;
+    hipGetDevice(&prev);
+    if (prev != s->device) hipSetDevice(s->device);
+    hipError_t e = nerve::launch_record_tokens(seen, seen_stride, rows, ids, ids_stride, counts, max_count,
+                                               s->desc.vocab_size, (hipStream_t)stream);
+    if (prev != s->device) hipSetDevice(prev);
+    if (e != hipSuccess) return hip_fail(e, "record_tokens launch");
+    return NERVE_OK;
+}
+
+int nerve_sampler_copy_token_state(nerve_sampler *s, uint32_t *dst, const uint32_t *src, uint32_t rows,
+                                   uint32_t seen_stride, void *stream) {
+    if (!s || !dst || !src) return fail(NERVE_ERR_INVALID_ARGUMENT, "null argument");
+    if (rows == 0u) return NERVE_OK;
+    hipError_t e = hipMemcpyAsync(dst, src, (size_t)rows * seen_stride * sizeof(uint32_t), hipMemcpyDeviceToDevice,
+                                  (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "copy_token_state");
+    return NERVE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,64 @@
+// nerve_sampler_internal.h -- launch arguments shared by the API and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "nerve_sampler.h"
+
+namespace nerve {
+
+enum : uint32_t {
+    kVariantF32Vec = 0,     // 16-byte loads, 4 f32 per load
+    kVariantBf16Vec = 1,    // 16-byte loads, 8 bf16 per load
+    kVariantF32Scalar = 2,  // unaligned rows: one element per load
+    kVariantBf16Scalar = 3,
+};
+
+struct StepArgs {
+    const void *logits;
+    uint64_t ld;
+    const nerve_sampler_row_params *params;
+    const uint32_t *history;
+    const uint32_t *history_len;
+    uint32_t history_stride;
+    const uint32_t *seen;
+    uint32_t seen_stride;
+    const uint32_t *allowed;
+    uint32_t allowed_stride;
+    const uint32_t *seeds;
+    const uint64_t *steps;
+    uint32_t *stream_control;
+    uint32_t *ring;
+    uint32_t ring_stride;
+    nerve_sampler_output *out;
+    uint32_t *topk_ids;
+    float *topk_logits;
+    float *topk_probs;
+    uint2 *scratch_lists;    // [max_batch][slices][kcap]
+    uint32_t *scratch_meta;  // [max_batch][slices]: count | flags << 16
+    uint32_t *counters;      // [max_batch], zero between launches
+    uint32_t vocab;
+    uint32_t batch;
+    uint32_t slices;
+    uint32_t kcap;
+    uint32_t rng;
+    uint32_t eos;
+    uint32_t nvec;           // vector slots per row
+    uint32_t vec_per_slice;
+    uint32_t hash_slots;     // power of two, 0 without a history
+    uint32_t log2_slots;
+    uint32_t big_entries;    // uint2 entries of the candidate / merge area
+    uint32_t dyn_lds_bytes;
+};
+
+uint32_t elems_per_thread(uint32_t variant);
+uint32_t elems_per_vector(uint32_t variant);
+uint32_t block_threads();
+uint32_t cand_capacity();
+hipError_t launch_sample_rows(uint32_t variant, const StepArgs &a, hipStream_t stream);
+hipError_t launch_record_tokens(uint32_t *seen, uint32_t seen_stride, uint32_t rows, const uint32_t *ids,
+                                uint32_t ids_stride, const uint32_t *counts, uint32_t max_count, uint32_t vocab,
+                                hipStream_t stream);
+
+}  // namespace nerve
