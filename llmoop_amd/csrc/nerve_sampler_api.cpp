@@ -58,7 +58,6 @@ struct nerve_sampler {
     uint32_t slices_capacity;  // scratch sized for this many
     uint2 *scratch_lists;
     uint32_t *scratch_meta;
-    uint32_t *counters;
     size_t lds_per_block;      // hipDeviceProp_t::sharedMemPerBlock
 };
 
@@ -194,24 +193,21 @@ int nerve_sampler_create(const nerve_sampler_desc *desc, nerve_sampler **out) {
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(NERVE_ERR_HIP, std::string("the sampler kernels are built for gfx950 only, device is ") + prop.gcnArchName);
 
-    // Slices per row: enough that one workgroup's share of the row fits its
-    // registers (checked again per step for the variant the alignment picks),
-    // and more when the batch is small so the launch still covers the CUs.
+    // Workgroups per row: one streams a whole row in stages; small batches
+    // split rows so the launch still covers the CUs (one workgroup per CU).
     const uint32_t threads = nerve::block_threads();
-    const uint32_t scalar_tokens_per_wg = threads * nerve::elems_per_thread(nerve::kVariantF32Scalar);
-    const uint32_t slices_worst = (d.vocab_size + scalar_tokens_per_wg - 1u) / scalar_tokens_per_wg;
     uint32_t want = d.slices_per_row;
     if (want == 0u) {
         const uint32_t cus = (uint32_t)prop.multiProcessorCount;
-        want = (2u * cus + d.max_batch - 1u) / d.max_batch;
-        const uint32_t by_size = d.vocab_size / (threads * 4u);  // keep >= ~4 elements per lane
+        want = cus / d.max_batch;
+        const uint32_t by_size = d.vocab_size / (threads * 16u);  // keep >= 16 elements per lane
         if (want > by_size) want = by_size;
         if (want > 64u) want = 64u;
-        const uint32_t by_merge = 12288u / d.top_k_capacity;  // merge area of the last workgroup
+        const uint32_t by_merge = 12288u / d.top_k_capacity;  // merge area of the finish kernel
         if (want > by_merge) want = by_merge;
         if (want == 0u) want = 1u;
     }
-    const uint32_t capacity = want > slices_worst ? want : slices_worst;
+    const uint32_t capacity = want;
     if ((uint64_t)capacity * d.top_k_capacity > 12288u)
         return fail(NERVE_ERR_INVALID_SAMPLING_SPEC, "slices_per_row * top_k_capacity exceeds the 12288-entry merge area");
 
@@ -223,17 +219,14 @@ int nerve_sampler_create(const nerve_sampler_desc *desc, nerve_sampler **out) {
     s->slices_capacity = capacity;
     s->lds_per_block = prop.sharedMemPerBlock;
     int prev = 0;
-    hipGetDevice(&prev);
-    hipSetDevice(s->device);
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(s->device);
     const size_t lists_bytes = (size_t)d.max_batch * capacity * d.top_k_capacity * sizeof(uint2);
     const size_t meta_bytes = (size_t)d.max_batch * capacity * sizeof(uint32_t);
-    const size_t counter_bytes = (size_t)d.max_batch * sizeof(uint32_t);
     e = hipMalloc((void **)&s->scratch_lists, lists_bytes);
     if (e == hipSuccess) e = hipMalloc((void **)&s->scratch_meta, meta_bytes);
-    if (e == hipSuccess) e = hipMalloc((void **)&s->counters, counter_bytes);
-    if (e == hipSuccess) e = hipMemset(s->counters, 0, counter_bytes);
     if (e == hipSuccess) e = hipDeviceSynchronize();
-    hipSetDevice(prev);
+    (void)hipSetDevice(prev);
     if (e != hipSuccess) {
         int rc = hip_fail(e, "nerve_sampler_create scratch");
         nerve_sampler_destroy(s);
@@ -246,12 +239,11 @@ int nerve_sampler_create(const nerve_sampler_desc *desc, nerve_sampler **out) {
 int nerve_sampler_destroy(nerve_sampler *s) {
     if (!s) return NERVE_OK;
     int prev = 0;
-    hipGetDevice(&prev);
-    hipSetDevice(s->device);
-    if (s->scratch_lists) hipFree(s->scratch_lists);
-    if (s->scratch_meta) hipFree(s->scratch_meta);
-    if (s->counters) hipFree(s->counters);
-    hipSetDevice(prev);
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(s->device);
+    if (s->scratch_lists) (void)hipFree(s->scratch_lists);
+    if (s->scratch_meta) (void)hipFree(s->scratch_meta);
+    (void)hipSetDevice(prev);
     delete s;
     return NERVE_OK;
 }
@@ -280,21 +272,16 @@ int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *str
 
     const size_t esize = d.dtype == NERVE_DTYPE_F32 ? 4u : 2u;
     const bool aligned = ((uintptr_t)b->logits % 16u == 0u) && ((b->logits_row_stride * esize) % 16u == 0u);
+    // 16-byte loads need an aligned row base and stride and at least one full slot.
+    const bool vec_ok = aligned && d.vocab_size >= (d.dtype == NERVE_DTYPE_F32 ? 4u : 8u);
     uint32_t variant;
-    if (d.dtype == NERVE_DTYPE_F32) variant = aligned ? nerve::kVariantF32Vec : nerve::kVariantF32Scalar;
-    else variant = aligned ? nerve::kVariantBf16Vec : nerve::kVariantBf16Scalar;
+    if (d.dtype == NERVE_DTYPE_F32) variant = vec_ok ? nerve::kVariantF32Vec : nerve::kVariantF32Scalar;
+    else variant = vec_ok ? nerve::kVariantBf16Vec : nerve::kVariantBf16Scalar;
 
     const uint32_t epv = nerve::elems_per_vector(variant);
-    const uint32_t per_thread = nerve::elems_per_thread(variant);
-    const uint32_t threads = nerve::block_threads();
-    const uint32_t nvec = (d.vocab_size + epv - 1u) / epv;
-    const uint32_t vec_budget = threads * (per_thread / epv);
-    uint32_t slices = s->slices;
-    const uint32_t slices_min = (nvec + vec_budget - 1u) / vec_budget;
-    if (slices < slices_min) slices = slices_min;
-    if (slices > s->slices_capacity) return fail(NERVE_ERR_INVALID_ARGUMENT, "slice count exceeds the scratch capacity");
+    const uint32_t nvec = d.vocab_size / epv;  // full slots; the V % epv tail goes to the last slice
+    const uint32_t slices = s->slices;
     const uint32_t vec_per_slice = (nvec + slices - 1u) / slices;
-    if (vec_per_slice > vec_budget) return fail(NERVE_ERR_INVALID_ARGUMENT, "slice exceeds one workgroup's register budget");
 
     nerve::StepArgs a;
     std::memset(&a, 0, sizeof(a));
@@ -319,7 +306,6 @@ int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *str
     a.topk_probs = b->topk_probs;
     a.scratch_lists = s->scratch_lists;
     a.scratch_meta = s->scratch_meta;
-    a.counters = s->counters;
     a.vocab = d.vocab_size;
     a.batch = b->batch;
     a.slices = slices;
@@ -333,19 +319,25 @@ int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *str
         if (a.hash_slots < 64u) a.hash_slots = 64u;
         a.log2_slots = log2u(a.hash_slots);
     }
-    uint32_t big = nerve::cand_capacity();
+    if (b->history) {
+        const uint32_t slice_tokens = vec_per_slice * epv + epv;
+        a.bitmap_words = ((slice_tokens + 31u) / 32u + 3u) & ~1u;
+    }
+    uint32_t big = nerve::merge_capacity();
     if (slices * d.top_k_capacity > big) big = slices * d.top_k_capacity;
     a.big_entries = big;
-    a.dyn_lds_bytes = a.hash_slots * 4u + big * 8u + d.top_k_capacity * 8u;
-    const size_t static_lds = 8u * 1024u;  // slice bitmap (<= 4 KiB) and reduction scratch
-    if (a.dyn_lds_bytes + static_lds > s->lds_per_block)
+    a.finish_lds_bytes = a.hash_slots * 4u + big * 8u + d.top_k_capacity * 8u;
+    const uint32_t stream_lds = nerve::stream_lds_bytes(variant, b->allowed != nullptr, b->seen != nullptr,
+                                                        a.hash_slots, a.bitmap_words, d.top_k_capacity);
+    const size_t static_lds = 2u * 1024u;  // reduction scratch
+    if (stream_lds + static_lds > s->lds_per_block || a.finish_lds_bytes + static_lds > s->lds_per_block)
         return fail(NERVE_ERR_INVALID_ARGUMENT, "LDS need of this top_k_capacity / history / slice count exceeds the device");
 
     int prev = 0;
-    hipGetDevice(&prev);
-    if (prev != s->device) hipSetDevice(s->device);
+    (void)hipGetDevice(&prev);
+    if (prev != s->device) (void)hipSetDevice(s->device);
     hipError_t e = nerve::launch_sample_rows(variant, a, (hipStream_t)stream);
-    if (prev != s->device) hipSetDevice(prev);
+    if (prev != s->device) (void)hipSetDevice(prev);
     if (e != hipSuccess) return hip_fail(e, "sample_rows launch");
     return NERVE_OK;
 }
@@ -363,11 +355,11 @@ int nerve_sampler_record_tokens(nerve_sampler *s, uint32_t *seen, uint32_t seen_
     if (rows == 0u) return NERVE_OK;
     if (seen_stride < (s->desc.vocab_size + 31u) / 32u) return fail(NERVE_ERR_INVALID_ARGUMENT, "seen_stride < ceil(vocab/32)");
     int prev = 0;
-    hipGetDevice(&prev);
-    if (prev != s->device) hipSetDevice(s->device);
+    (void)hipGetDevice(&prev);
+    if (prev != s->device) (void)hipSetDevice(s->device);
     hipError_t e = nerve::launch_record_tokens(seen, seen_stride, rows, ids, ids_stride, counts, max_count,
                                                s->desc.vocab_size, (hipStream_t)stream);
-    if (prev != s->device) hipSetDevice(prev);
+    if (prev != s->device) (void)hipSetDevice(prev);
     if (e != hipSuccess) return hip_fail(e, "record_tokens launch");
     return NERVE_OK;
 }

@@ -35,27 +35,29 @@ struct StepArgs {
     uint32_t *topk_ids;
     float *topk_logits;
     float *topk_probs;
-    uint2 *scratch_lists;    // [max_batch][slices][kcap]
+    uint2 *scratch_lists;    // [max_batch][slices][kcap] sorted slice survivors
     uint32_t *scratch_meta;  // [max_batch][slices]: count | flags << 16
-    uint32_t *counters;      // [max_batch], zero between launches
     uint32_t vocab;
     uint32_t batch;
     uint32_t slices;
     uint32_t kcap;
     uint32_t rng;
     uint32_t eos;
-    uint32_t nvec;           // vector slots per row
+    uint32_t nvec;           // full vector slots per row (vocab / elements per slot)
     uint32_t vec_per_slice;
     uint32_t hash_slots;     // power of two, 0 without a history
     uint32_t log2_slots;
+    uint32_t bitmap_words;   // LDS words of the slice's history bitmap (even; 0 without a history)
     uint32_t big_entries;    // uint2 entries of the candidate / merge area
-    uint32_t dyn_lds_bytes;
+    uint32_t dyn_lds_bytes;     // slice kernel
+    uint32_t finish_lds_bytes;  // finish kernel (slices > 1)
 };
 
-uint32_t elems_per_thread(uint32_t variant);
 uint32_t elems_per_vector(uint32_t variant);
 uint32_t block_threads();
-uint32_t cand_capacity();
+uint32_t merge_capacity();
+uint32_t stream_lds_bytes(uint32_t variant, bool mask, bool seen, uint32_t hash_slots, uint32_t bitmap_words,
+                          uint32_t kcap);
 hipError_t launch_sample_rows(uint32_t variant, const StepArgs &a, hipStream_t stream);
 hipError_t launch_record_tokens(uint32_t *seen, uint32_t seen_stride, uint32_t rows, const uint32_t *ids,
                                 uint32_t ids_stride, const uint32_t *counts, uint32_t max_count, uint32_t vocab,

@@ -1,24 +1,27 @@
-// nerve_sampler_kernels.hip -- the fused gfx950 sampling kernel and its launcher.
+// nerve_sampler_kernels.hip -- the gfx950 sampling kernels and their launcher.
 //
-// One launch samples every row of a decode batch. Each row is split into S
-// vocabulary slices, one 512-lane workgroup per slice (S*B workgroups in all,
-// mapped so the slices of one row land on one XCD and share its L2):
-//
-//   1. history ids of the row that fall in the slice go into an LDS bitmap and
-//      an LDS id->count hash (penalties are looked up only where a bit is set);
-//   2. the slice streams from HBM once with 16-byte loads, all loads of a lane
-//      issued before the first is consumed, and stays in VGPRs as order keys
-//      (mask, penalties, NaN and -inf exclusion applied on the fly);
-//   3. top-k: an 8+8-bit LDS radix select over the 512 per-lane maxima gives a
-//      threshold t with at least k keys >= t; for iid logits about k+3 keys
-//      pass it. They are compacted to LDS and rank-sorted (value desc, id asc).
-//      A skewed slice (more than kCandCap survivors) falls back to an exact
-//      4-pass radix select on all keys plus an id-ordered tie cut;
-//   4. the sorted slice list goes to scratch; the last workgroup of the row
-//      (device-scope counter) merges the S lists by binary-search ranks, then
-//      one wave runs min-p / top-p over the k survivors and the draw, and
-//      writes the output record (and, if asked, survivors, probabilities,
-//      stream control and the output ring).
+// One step samples every row of a decode batch with at most two launches.
+// sample_rows_kernel: each row is split into S vocabulary slices, one 512-lane
+// workgroup per slice (mapped so the slices of a row share one XCD's L2). A
+// workgroup streams its slice from HBM once, in chunks of 8 x 16-byte loads per
+// lane, double-buffered in VGPRs so the loads of chunk c+1 are in flight while
+// chunk c is processed:
+//   - history ids of the slice go into an LDS bitmap and an id -> count hash;
+//     a token with penalty state leaves the stream and re-enters as a patch
+//     entry carrying its configured (masked + penalised) value;
+//   - every other element becomes an order key straight from its raw bits;
+//   - greedy rows keep a per-lane best; sampled rows take a threshold from the
+//     first chunk (the k-th largest per-lane maximum, 16-bit LDS radix select:
+//     at least k keys are >= it) and append every later key >= it to an LDS
+//     candidate list with wave-ballot compaction (about k + a few per chunk
+//     for iid logits). A list that would overflow switches the slice to an
+//     exact radix selection recomputed from memory;
+//   - the candidates are rank-sorted (value desc, id asc) into the slice's
+//     top-k list.
+// With S = 1 the workgroup finishes the row itself; otherwise it writes the
+// list to scratch and finish_rows_kernel (one workgroup per row, same stream,
+// so no cross-workgroup fence) merges the S lists by binary-search ranks, then
+// one wave runs min-p / top-p over the k survivors and the draw.
 //
 // Semantics follow the reference shaders (paths under runtime-rs/shaders/):
 //   greedy_sampler_f32.comp.template:31-34, 52-108       tie-break, argmax, record, tick carry
@@ -35,12 +38,41 @@
 
 namespace nerve {
 
+#ifdef NERVE_PHASE_TIMING
+// Profiling builds only: per-workgroup shader-clock stamps at phase boundaries.
+__device__ uint64_t g_phase_ts[16384 * 8];
+#define PHASE_MARK(i)                                                                        \
+    do {                                                                                     \
+        if (threadIdx.x == 0 && blockIdx.x < 16384u)                                         \
+            g_phase_ts[blockIdx.x * 8u + (i)] = __builtin_amdgcn_s_memtime();                \
+    } while (0)
+__device__ uint32_t g_dbg[16384 * 4];
+#define DBG_ADD(i, v) atomicAdd(&g_dbg[blockIdx.x * 4u + (i)], (v))
+#define DBG_SET(i, v) (g_dbg[blockIdx.x * 4u + (i)] = (v))
+#else
+#define DBG_ADD(i, v) ((void)0)
+#define DBG_SET(i, v) ((void)0)
+#define PHASE_MARK(i) \
+    do {              \
+    } while (0)
+#endif
+
 constexpr int kBlock = 512;
 constexpr int kWaves = kBlock / 64;
+constexpr int kFinishBlock = 256;
 constexpr uint32_t kCandCap = 1024;
 constexpr uint32_t kHashEmpty = 0xffffffffu;
+constexpr uint32_t kMaxHistory = NERVE_MAX_HISTORY_CAPACITY;
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+// Workgroup barrier that orders LDS only: waits for this wave's LDS traffic,
+// not for its global loads, so prefetched chunks stay in flight across it.
+__device__ __forceinline__ void lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 __device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
     const uint32_t lane = lane_id();
@@ -74,7 +106,7 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *s
     const uint32_t tid = threadIdx.x, wave = tid >> 6;
     uint32_t inc = wave_inclusive_scan(v);
     if (lane_id() == 63) s_tmp[wave] = inc;
-    __syncthreads();
+    lds_sync();
     uint32_t base = 0, tot = 0;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
@@ -82,7 +114,7 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *s
         base += (uint32_t)w < wave ? t : 0u;
         tot += t;
     }
-    __syncthreads();
+    lds_sync();
     total = tot;
     return base + inc - v;
 }
@@ -96,12 +128,20 @@ __device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t *s_tmp) {
 __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t *s_tmp) {
     v = wave_max_u64(v);
     if (lane_id() == 0) s_tmp[threadIdx.x >> 6] = v;
-    __syncthreads();
+    lds_sync();
     uint64_t m = s_tmp[0];
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) m = s_tmp[w] > m ? s_tmp[w] : m;
-    __syncthreads();
+    lds_sync();
     return m;
+}
+
+// Order key of a binary32 bit pattern (same mapping as order_key()).
+__device__ __forceinline__ uint32_t raw_order_key(uint32_t bits) {
+    const uint32_t mag = bits & 0x7fffffffu;
+    const uint32_t b = mag == 0u ? 0u : bits;
+    const uint32_t key = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return mag > 0x7f800000u ? 0u : key;
 }
 
 __device__ __forceinline__ bool entry_better(uint2 a, uint2 b) {
@@ -118,7 +158,7 @@ __device__ __forceinline__ uint32_t hash_slot(uint32_t id, uint32_t log2_slots) 
     return (id * 0x9E3779B1u) >> (32u - log2_slots);
 }
 
-__device__ void hash_insert(uint32_t *h, uint32_t log2_slots, uint32_t id) {
+__device__ __forceinline__ void hash_insert(uint32_t *h, uint32_t log2_slots, uint32_t id) {
     const uint32_t mask = (1u << log2_slots) - 1u;
     uint32_t slot = hash_slot(id, log2_slots);
     for (uint32_t probe = 0; probe <= mask; ++probe) {
@@ -163,25 +203,94 @@ __device__ __forceinline__ float load_elem<uint16_t>(const uint16_t *row, uint32
     return u2f((uint32_t)row[t] << 16);
 }
 
-// Raw words of one EPV-element vector slot: W = EPV*sizeof(Elem)/4 words (min 1).
-template <typename Elem, int EPV>
-struct VecTraits {
-    static constexpr int W = (EPV * (int)sizeof(Elem) + 3) / 4;
-};
+// One EPV-element slot as loaded from HBM (16 bytes for the vector variants).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <typename Elem, int EPV>
-__device__ __forceinline__ float raw_elem(const uint32_t (&r)[VecTraits<Elem, EPV>::W], int e) {
-    if constexpr (sizeof(Elem) == 4) {
-        return u2f(r[e]);
-    } else {
-        if constexpr (EPV == 1) {
-            return u2f(r[0] << 16);
-        } else {
-            uint32_t w = r[e >> 1];
-            return u2f((e & 1) ? (w & 0xffff0000u) : (w << 16));
-        }
-    }
+struct VecTraits;
+
+// bits(): the binary32 bit pattern of element e (bf16 widens exactly by a shift).
+// upper(): an upper bound of the canonical order keys of the lane-vector's raw
+// values (exact except that -0.0 is lifted to +0.0's key), computed with packed
+// integer ops; has_nan(): whether any raw value is a NaN.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x2 __attribute__((ext_vector_type(2)));
+
+// Order keys of two bf16 values at once: negative -> ~h, else h | 0x8000.
+__device__ __forceinline__ uint32_t bf16x2_keys(uint32_t w) {
+    const i16x2 s = __builtin_bit_cast(i16x2, w) >> (i16x2){15, 15};
+    return w ^ (__builtin_bit_cast(uint32_t, s) | 0x80008000u);
 }
+
+__device__ __forceinline__ uint32_t u16x2_max(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+
+__device__ __forceinline__ uint32_t f32_key_upper(uint32_t w) {
+    const uint32_t key = w ^ ((uint32_t)((int32_t)w >> 31) | 0x80000000u);
+    return key == 0x7fffffffu ? 0x80000000u : key;
+}
+template <>
+struct VecTraits<float, 4> {
+    using load_t = u32x4;
+    __device__ static __forceinline__ uint32_t upper(const load_t &r) {
+        const uint32_t a = max(f32_key_upper(r[0]), f32_key_upper(r[1]));
+        const uint32_t b = max(f32_key_upper(r[2]), f32_key_upper(r[3]));
+        return max(a, b);
+    }
+    __device__ static __forceinline__ bool has_nan(const load_t &r) {
+        const uint32_t m = max(max(r[0] & 0x7fffffffu, r[1] & 0x7fffffffu), max(r[2] & 0x7fffffffu, r[3] & 0x7fffffffu));
+        return m > 0x7f800000u;
+    }
+    __device__ static __forceinline__ uint32_t bits(const load_t &r, int e) { return r[e]; }
+    __device__ static __forceinline__ uint32_t bits_dyn(const load_t &r, uint32_t e) {
+        const uint32_t lo = (e & 1u) ? r[1] : r[0], hi = (e & 1u) ? r[3] : r[2];
+        return (e & 2u) ? hi : lo;
+    }
+};
+
+template <>
+struct VecTraits<uint16_t, 8> {
+    using load_t = u32x4;
+    __device__ static __forceinline__ uint32_t upper(const load_t &r) {
+        const uint32_t m2 = u16x2_max(u16x2_max(bf16x2_keys(r[0]), bf16x2_keys(r[1])),
+                                      u16x2_max(bf16x2_keys(r[2]), bf16x2_keys(r[3])));
+        const uint32_t m16 = max(m2 & 0xffffu, m2 >> 16);
+        return m16 == 0x7fffu ? 0x80000000u : ((m16 << 16) | 0xffffu);
+    }
+    __device__ static __forceinline__ bool has_nan(const load_t &r) {
+        const uint32_t t = ((r[0] & 0x7fff7fffu) + 0x007f007fu) | ((r[1] & 0x7fff7fffu) + 0x007f007fu) |
+                           ((r[2] & 0x7fff7fffu) + 0x007f007fu) | ((r[3] & 0x7fff7fffu) + 0x007f007fu);
+        return (t & 0x80008000u) != 0u;
+    }
+    __device__ static __forceinline__ uint32_t bits(const load_t &r, int e) {
+        const uint32_t w = r[e >> 1];
+        return (e & 1) ? (w & 0xffff0000u) : (w << 16);
+    }
+    __device__ static __forceinline__ uint32_t bits_dyn(const load_t &r, uint32_t e) {
+        const uint32_t lo = (e & 2u) ? r[1] : r[0], hi = (e & 2u) ? r[3] : r[2];
+        const uint32_t w = (e & 4u) ? hi : lo;
+        return (e & 1u) ? (w & 0xffff0000u) : (w << 16);
+    }
+};
+
+template <>
+struct VecTraits<float, 1> {
+    using load_t = float;
+    __device__ static __forceinline__ uint32_t upper(const load_t &r) { return f32_key_upper(f2u(r)); }
+    __device__ static __forceinline__ bool has_nan(const load_t &r) { return (f2u(r) & 0x7fffffffu) > 0x7f800000u; }
+    __device__ static __forceinline__ uint32_t bits(const load_t &r, int) { return f2u(r); }
+    __device__ static __forceinline__ uint32_t bits_dyn(const load_t &r, uint32_t) { return f2u(r); }
+};
+
+template <>
+struct VecTraits<uint16_t, 1> {
+    using load_t = uint16_t;
+    __device__ static __forceinline__ uint32_t upper(const load_t &r) { return f32_key_upper((uint32_t)r << 16); }
+    __device__ static __forceinline__ bool has_nan(const load_t &r) { return ((uint32_t)r & 0x7fffu) > 0x7f80u; }
+    __device__ static __forceinline__ uint32_t bits(const load_t &r, int) { return (uint32_t)r << 16; }
+    __device__ static __forceinline__ uint32_t bits_dyn(const load_t &r, uint32_t) { return (uint32_t)r << 16; }
+};
 
 // Row state shared by the helpers that recompute a single configured value.
 struct RowCtx {
@@ -197,7 +306,7 @@ struct RowCtx {
 };
 
 template <typename Elem>
-__device__ float configured_at(const RowCtx &c, uint32_t t) {
+__device__ __forceinline__ float configured_at(const RowCtx &c, uint32_t t) {
     float x = load_elem<Elem>((const Elem *)c.logits_row, t);
     bool allowed = c.allowed_row ? ((c.allowed_row[t >> 5] >> (t & 31u)) & 1u) : true;
     uint32_t count = 0;
@@ -225,7 +334,7 @@ __device__ __forceinline__ bool float_better(float cl, uint32_t cid, float bl, u
 // nonzero key") when fewer than k keys are nonzero. `count_ge` receives the
 // number of keys >= t when passes == 4 or the fewer-than-k case applies.
 template <int N>
-__device__ uint32_t radix_threshold(const uint32_t (&v)[N], uint32_t k, int passes, uint32_t *s_hist,
+__device__ __forceinline__ uint32_t radix_threshold(const uint32_t (&v)[N], uint32_t k, int passes, uint32_t *s_hist,
                                     uint32_t *s_sel, uint32_t &count_ge) {
     const uint32_t tid = threadIdx.x;
     uint32_t prefix = 0, remaining = k, above_total = 0;
@@ -234,13 +343,13 @@ __device__ uint32_t radix_threshold(const uint32_t (&v)[N], uint32_t k, int pass
         const int shift = 24 - 8 * p;
         const uint32_t hmask = p == 0 ? 0u : (0xffffffffu << (shift + 8));
         for (uint32_t i = tid; i < 256u; i += kBlock) s_hist[i] = 0u;
-        __syncthreads();
+        lds_sync();
 #pragma unroll
         for (int i = 0; i < N; ++i) {
             uint32_t x = v[i];
             if (x != 0u && (x & hmask) == prefix) atomicAdd(&s_hist[(x >> shift) & 255u], 1u);
         }
-        __syncthreads();
+        lds_sync();
         if (tid < 64) {
             const uint32_t lane = tid;
             uint32_t c[4], sum = 0;
@@ -268,9 +377,9 @@ __device__ uint32_t radix_threshold(const uint32_t (&v)[N], uint32_t k, int pass
                 s_sel[1] = incl;
             }
         }
-        __syncthreads();
+        lds_sync();
         const uint32_t d = s_sel[0], above = s_sel[1], in_bin = s_sel[2];
-        __syncthreads();
+        lds_sync();
         if (d == 0xffffffffu) {
             count_ge = above_total + above;
             return 1u;
@@ -287,7 +396,7 @@ __device__ uint32_t radix_threshold(const uint32_t (&v)[N], uint32_t k, int pass
 // [t0, t1) of a slice with keys produced by `key_of(t)`; used by the rare
 // exact path, which recomputes keys from memory instead of holding them.
 template <typename KeyFn>
-__device__ uint32_t radix_threshold_fn(uint32_t t0, uint32_t t1, uint32_t k, uint32_t *s_hist, uint32_t *s_sel,
+__device__ __forceinline__ uint32_t radix_threshold_fn(uint32_t t0, uint32_t t1, uint32_t k, uint32_t *s_hist, uint32_t *s_sel,
                                        uint32_t &count_ge, KeyFn key_of) {
     const uint32_t tid = threadIdx.x;
     uint32_t prefix = 0, remaining = k, above_total = 0;
@@ -296,12 +405,12 @@ __device__ uint32_t radix_threshold_fn(uint32_t t0, uint32_t t1, uint32_t k, uin
         const int shift = 24 - 8 * p;
         const uint32_t hmask = p == 0 ? 0u : (0xffffffffu << (shift + 8));
         for (uint32_t i = tid; i < 256u; i += kBlock) s_hist[i] = 0u;
-        __syncthreads();
+        lds_sync();
         for (uint32_t t = t0 + tid; t < t1; t += kBlock) {
             const uint32_t x = key_of(t);
             if (x != 0u && (x & hmask) == prefix) atomicAdd(&s_hist[(x >> shift) & 255u], 1u);
         }
-        __syncthreads();
+        lds_sync();
         if (tid < 64) {
             const uint32_t lane = tid;
             uint32_t c[4], sum = 0;
@@ -329,9 +438,9 @@ __device__ uint32_t radix_threshold_fn(uint32_t t0, uint32_t t1, uint32_t k, uin
                 s_sel[1] = incl;
             }
         }
-        __syncthreads();
+        lds_sync();
         const uint32_t d = s_sel[0], above = s_sel[1], in_bin = s_sel[2];
-        __syncthreads();
+        lds_sync();
         if (d == 0xffffffffu) {
             count_ge = above_total + above;
             return 1u;
@@ -362,320 +471,52 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t n) {
     return xcd < rem ? xcd * (q + 1u) + idx : rem * (q + 1u) + (xcd - rem) * q + idx;
 }
 
-// PEN: 0 = no penalty state, 1 = seen bitmap (set semantics), 2 = history ids (count semantics).
-template <typename Elem, int EPV, int NV, bool MASK, int PEN>
-__global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
-    constexpr int E = NV * EPV;
-    constexpr int W = VecTraits<Elem, EPV>::W;
-    __shared__ SharedSmall sm;
-    __shared__ uint32_t s_bitmap[kBlock * E / 32];
-    extern __shared__ uint32_t s_dyn[];
-    uint32_t *s_hash = s_dyn;                                        // [hash_slots]
-    uint2 *s_big = (uint2 *)(s_dyn + a.hash_slots);                   // [big_entries]
-    uint2 *s_sorted = s_big + a.big_entries;                          // [kcap]
-
+// Finishes one row from its sorted survivors s_sorted[0 .. n) (value desc,
+// id asc): EOS fallback for an all-zero mask, the greedy record (replaying the
+// reference's 1024-lane argmax when the row holds a NaN), or min-p / top-p over
+// the k survivors and the draw (temperature_top_k_top_p_sampler_f32:157-216).
+// Writes the output record, optional survivors / probabilities, the stream
+// control tick and the output ring. Runs on NT threads; wave 0 does the
+// sequential running sums.
+template <typename Elem, int PEN, int NT>
+__device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, const nerve_sampler_row_params &P, uint32_t k,
+                           bool sampled, uint32_t n, uint32_t row_flags, uint2 *s_sorted, uint2 *s_big,
+                           uint32_t *s_hash, const RowCtx &ctx) {
+    __shared__ uint32_t s_res[2];
     const uint32_t tid = threadIdx.x;
-    const uint32_t logical = xcd_remap(blockIdx.x, gridDim.x);
-    const uint32_t row = logical / a.slices;
-    const uint32_t slice = logical % a.slices;
-
-    const nerve_sampler_row_params P = a.params[row];
-    const bool sampled = P.method != NERVE_METHOD_GREEDY;
-    uint32_t k = sampled ? P.top_k : 1u;
-    k = k < 1u ? 1u : (k > a.kcap ? a.kcap : k);
-    const uint32_t valid_min = sampled ? kMinFiniteKey : kNegInfKey;
-
-    const uint32_t v0 = slice * a.vec_per_slice;
-    const uint32_t v1 = min(v0 + a.vec_per_slice, a.nvec);
-    const uint32_t tok0 = v0 * EPV;
-    const uint32_t tok1 = min(v1 * EPV, a.vocab);
-
-    const Elem *lrow = (const Elem *)a.logits + (uint64_t)row * a.ld;
-    const uint32_t *arow = MASK ? a.allowed + (uint64_t)row * a.allowed_stride : nullptr;
-    const uint32_t *srow = PEN == 1 ? a.seen + (uint64_t)row * a.seen_stride : nullptr;
-    constexpr bool history = PEN == 2;
-
-    // 1. penalty tables for this slice
-    if constexpr (history) {
-        const uint32_t nslots = a.hash_slots;
-        for (uint32_t i = tid; i < nslots; i += kBlock) s_hash[i] = kHashEmpty;
-        const uint32_t nbw = (tok1 - tok0 + 31u) / 32u;
-        for (uint32_t i = tid; i < nbw; i += kBlock) s_bitmap[i] = 0u;
-        __syncthreads();
-        uint32_t len = a.history_len[row];
-        len = len > a.history_stride ? a.history_stride : len;
-        const uint32_t *hrow = a.history + (uint64_t)row * a.history_stride;
-        for (uint32_t i = tid; i < len; i += kBlock) {
-            uint32_t id = hrow[i];
-            if (id >= tok0 && id < tok1) {
-                uint32_t o = id - tok0;
-                atomicOr(&s_bitmap[o >> 5], 1u << (o & 31u));
-                hash_insert(s_hash, a.log2_slots, id);
-            }
-        }
-        __syncthreads();
-    }
-
-    // 2. stream the slice once into registers
-    uint32_t raw[NV][W];
-    uint32_t mword[MASK ? NV : 1], sword[PEN == 1 ? NV : 1];
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const uint32_t slot = v0 + (uint32_t)j * kBlock + tid;
-        const uint32_t id0 = slot * EPV;
-#pragma unroll
-        for (int w = 0; w < W; ++w) raw[j][w] = 0u;
-        if (slot < v1) {
-            if constexpr (EPV > 1) {
-                if (id0 + EPV <= a.vocab) {
-                    uint4 q = *(const uint4 *)(lrow + id0);
-                    raw[j][0] = q.x; raw[j][1] = q.y; raw[j][2] = q.z; raw[j][3] = q.w;
-                } else {
-#pragma unroll
-                    for (int e = 0; e < EPV; ++e) {
-                        if (id0 + e < a.vocab) {
-                            uint32_t bits = sizeof(Elem) == 4 ? f2u(load_elem<Elem>(lrow, id0 + e))
-                                                              : (f2u(load_elem<Elem>(lrow, id0 + e)) >> 16);
-                            if constexpr (sizeof(Elem) == 4) raw[j][e] = bits;
-                            else raw[j][e >> 1] |= (e & 1) ? (bits << 16) : bits;
-                        }
-                    }
-                }
-            } else {
-                if constexpr (sizeof(Elem) == 4) raw[j][0] = f2u(lrow[id0]);
-                else raw[j][0] = (uint32_t)lrow[id0];
-            }
-        }
-        if constexpr (MASK) mword[j] = slot < v1 ? arow[id0 >> 5] : 0u;
-        if constexpr (PEN == 1) sword[j] = slot < v1 ? srow[id0 >> 5] : 0u;
-    }
-
-    // keys, per-lane max (sampled) or best (greedy), slice flags
-    uint32_t keys[E];
-    uint32_t tmax = 0, best_id = kPadId;
-    uint32_t any_allowed = 0, has_nan = 0;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const uint32_t slot = v0 + (uint32_t)j * kBlock + tid;
-        const uint32_t id0 = slot * EPV;
-        uint32_t hb = 0u;
-        if constexpr (history) hb = slot < v1 ? s_bitmap[(id0 - tok0) >> 5] >> ((id0 - tok0) & 31u) : 0u;
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) {
-            const uint32_t id = id0 + (uint32_t)e;
-            const bool valid = slot < v1 && id < a.vocab;
-            const float x = raw_elem<Elem, EPV>(raw[j], e);
-            bool allowed = true;
-            if constexpr (MASK) allowed = (mword[j] >> (id & 31u)) & 1u;
-            uint32_t count = 0;
-            if constexpr (history) {
-                if ((hb >> e) & 1u) count = hash_lookup(s_hash, a.log2_slots, id);
-            } else if constexpr (PEN == 1) {
-                count = (sword[j] >> (id & 31u)) & 1u;
-            }
-            const float v = configured_logit(x, allowed, count, P.repetition_penalty, P.frequency_penalty,
-                                             P.presence_penalty);
-            uint32_t key = order_key(v);
-            if (valid && allowed) any_allowed = 1u;
-            if (valid && v != v) has_nan = 1u;
-            if (!valid || key < valid_min) key = 0u;
-            keys[j * EPV + e] = key;
-            if (key > tmax) {
-                tmax = key;
-                best_id = id;
-            }
-        }
-    }
-
-    RowCtx ctx;
-    ctx.logits_row = lrow;
-    ctx.allowed_row = arow;
-    ctx.seen_row = srow;
-    ctx.hash = s_hash;
-    ctx.bitmap = s_bitmap;
-    ctx.log2_slots = a.log2_slots;
-    ctx.tok0 = tok0;
-    ctx.rep = P.repetition_penalty;
-    ctx.freq = P.frequency_penalty;
-    ctx.pres = P.presence_penalty;
-    ctx.history = history;
-
-    // slice flags: bit 0 = some token allowed, bit 1 = some configured value is NaN
-    const uint32_t fsum = block_sum(any_allowed | (has_nan << 16), sm.scan);
-    const uint32_t flags_slice = ((fsum & 0xffffu) ? 1u : 0u) | ((fsum >> 16) ? 2u : 0u);
-
-    // 3. selection -> s_sorted[0 .. n_out)
-    uint32_t n_out = 0;
-    if (!sampled) {
-        uint64_t packed = tmax ? (((uint64_t)tmax << 32) | (uint64_t)(~best_id)) : 0ull;
-        uint64_t m = block_max_u64(packed, sm.red);
-        if (m != 0ull) {
-            if (tid == 0) s_sorted[0] = make_uint2((uint32_t)(m >> 32), ~(uint32_t)m);
-            n_out = 1;
-        }
-        __syncthreads();
-    } else {
-        uint32_t cnt_unused;
-        const uint32_t tm[1] = {tmax};
-        uint32_t t = radix_threshold<1>(tm, k, 2, sm.hist, sm.sel, cnt_unused);
-        uint32_t c = 0;
-#pragma unroll
-        for (int i = 0; i < E; ++i) c += keys[i] >= t ? 1u : 0u;
-        uint32_t C;
-        uint32_t base = block_exclusive_scan(c, sm.scan, C);
-        uint2 *s_cand = s_big;
-        if (C <= kCandCap) {
-            uint32_t pos = base;
-#pragma unroll
-            for (int i = 0; i < E; ++i) {
-                if (keys[i] >= t) {
-                    const uint32_t id = (v0 + (uint32_t)(i / EPV) * kBlock + tid) * EPV + (uint32_t)(i % EPV);
-                    s_cand[pos++] = make_uint2(keys[i], id);
-                }
-            }
-        } else {
-            // Skewed slice: exact selection recomputed from memory (rare). The
-            // k-th largest key kv, then the `need` smallest ids among keys == kv.
-            auto key_at = [&](uint32_t t) -> uint32_t {
-                uint32_t key = order_key(configured_at<Elem>(ctx, t));
-                return key < valid_min ? 0u : key;
-            };
-            uint32_t count_ge;
-            const uint32_t kv = radix_threshold_fn(tok0, tok1, k, sm.hist, sm.sel, count_ge, key_at);
-            uint32_t gt = 0;
-            for (uint32_t t = tok0 + tid; t < tok1; t += kBlock) gt += key_at(t) > kv ? 1u : 0u;
-            const uint32_t G = block_sum(gt, sm.scan);
-            const uint32_t need = k - G;  // count_ge >= k > G here
-            auto tie_at = [&](uint32_t t) -> uint32_t { return key_at(t) == kv ? ~t : 0u; };
-            uint32_t ties_ge;
-            const uint32_t id_cut = ~radix_threshold_fn(tok0, tok1, need, sm.hist, sm.sel, ties_ge, tie_at);
-            if (tid == 0) sm.flag[1] = 0u;
-            __syncthreads();
-            for (uint32_t t = tok0 + tid; t < tok1; t += kBlock) {
-                const uint32_t key = key_at(t);
-                if (key > kv || (key == kv && t <= id_cut)) {
-                    const uint32_t pos = atomicAdd(&sm.flag[1], 1u);
-                    if (pos < kCandCap) s_cand[pos] = make_uint2(key, t);
-                }
-            }
-            __syncthreads();
-            C = min(sm.flag[1], kCandCap);
-        }
-        __syncthreads();
-        // rank sort (ids are distinct, so ranks are a permutation)
-        for (uint32_t i = tid; i < C; i += kBlock) {
-            const uint2 e = s_cand[i];
-            uint32_t r = 0;
-            for (uint32_t j = 0; j < C; ++j) r += entry_better(s_cand[j], e) ? 1u : 0u;
-            if (r < k) s_sorted[r] = e;
-        }
-        n_out = C < k ? C : k;
-        __syncthreads();
-    }
-
-    // the sign of a zero survivor comes from its own configured value
-    for (uint32_t i = tid; i < n_out; i += kBlock) {
-        uint2 e = s_sorted[i];
-        if (e.x == kZeroKey) {
-            float v = configured_at<Elem>(ctx, e.y);
-            if (f2u(v) == 0x80000000u) s_sorted[i].y = e.y | kNegZeroFlag;
-        }
-    }
-    __syncthreads();
-
-    // 4. publish / merge
-    uint32_t n = n_out;
-    uint32_t row_flags = flags_slice;
-    if (a.slices > 1) {
-        uint2 *lists = a.scratch_lists + (uint64_t)(row * a.slices + slice) * a.kcap;
-        for (uint32_t i = tid; i < n_out; i += kBlock) lists[i] = s_sorted[i];
-        if (tid == 0) a.scratch_meta[row * a.slices + slice] = n_out | (flags_slice << 16);
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) {
-            uint32_t old = atomicAdd(&a.counters[row], 1u);
-            sm.flag[0] = old == a.slices - 1u ? 1u : 0u;
-        }
-        __syncthreads();
-        if (!sm.flag[0]) return;
-        __threadfence();
-        if (tid == 0) a.counters[row] = 0u;
-        const uint2 *all = a.scratch_lists + (uint64_t)row * a.slices * a.kcap;
-        const uint32_t *meta = a.scratch_meta + row * a.slices;
-        uint32_t total = 0;
-        row_flags = 0;
-        for (uint32_t s = 0; s < a.slices; ++s) {
-            uint32_t m = meta[s];
-            total += m & 0xffffu;
-            row_flags |= m >> 16;
-        }
-        const uint32_t ne = a.slices * a.kcap;
-        for (uint32_t i = tid; i < ne; i += kBlock) {
-            const uint32_t s = i / a.kcap, pos = i % a.kcap;
-            const uint32_t ns = meta[s] & 0xffffu;
-            if (pos < ns) s_big[i] = all[i];
-        }
-        __syncthreads();
-        for (uint32_t i = tid; i < ne; i += kBlock) {
-            const uint32_t s = i / a.kcap, pos = i % a.kcap;
-            const uint32_t ns = meta[s] & 0xffffu;
-            if (pos >= ns) continue;
-            const uint2 e = s_big[i];
-            uint32_t r = pos;
-            for (uint32_t o = 0; o < a.slices && r < k; ++o) {
-                if (o == s) continue;
-                const uint2 *lo = s_big + o * a.kcap;
-                uint32_t lo_i = 0, hi_i = meta[o] & 0xffffu;
-                while (lo_i < hi_i) {
-                    uint32_t mid = (lo_i + hi_i) >> 1;
-                    if (entry_better(lo[mid], e)) lo_i = mid + 1; else hi_i = mid;
-                }
-                r += lo_i;
-            }
-            if (r < k) s_sorted[r] = e;
-        }
-        n = total < k ? total : k;
-        __syncthreads();
-    }
-
-    // 5. final step for the row
-    float *s_w = (float *)s_big;               // [kcap] weights
-    float *s_p = (float *)s_big + a.kcap;      // [kcap] running sums
-    uint32_t token = 0, sel_bits = 0, out_flags = 0;
-    uint32_t kout = 1;                         // survivors to report
-    __shared__ uint32_t s_res[4];
+    float *s_w = (float *)s_big;           // [kcap] weights
+    float *s_p = (float *)s_big + a.kcap;  // [kcap] running sums, then probabilities
+    uint32_t token = 0, sel_bits = 0, out_flags = 0, kout = 1;
+    uint32_t *sc = a.stream_control ? a.stream_control + (uint64_t)row * 5u : nullptr;
 
     const bool eos = a.allowed && !(row_flags & 1u);
     if (eos) {
         token = a.eos;
-        sel_bits = 0xff800000u;
+        sel_bits = 0xff800000u;  // -inf: every token was masked
         out_flags = NERVE_FLAG_EOS_FALLBACK | (sampled ? NERVE_FLAG_SAMPLED : 0u);
-        if (tid == 0) {
-            s_sorted[0] = make_uint2(0u, a.eos);  // reported as (LOWEST_FLOAT, eos), prob 1
-            s_p[0] = 1.0f;
-        }
-        kout = 1;
+        if (tid == 0) s_p[0] = 1.0f;
     } else if (!sampled) {
         if (row_flags & 2u) {
-            // NaN present: replay the reference lane structure exactly.
-            if (history) {
-                for (uint32_t i = tid; i < a.hash_slots; i += kBlock) s_hash[i] = kHashEmpty;
+            // A NaN in the row: replay the reference lane structure exactly
+            // (greedy_sampler_f32:52-83), with penalties for the whole row.
+            if constexpr (PEN == 2) {
+                for (uint32_t i = tid; i < a.hash_slots; i += NT) s_hash[i] = kHashEmpty;
                 __syncthreads();
                 uint32_t len = a.history_len[row];
                 len = len > a.history_stride ? a.history_stride : len;
                 const uint32_t *hrow = a.history + (uint64_t)row * a.history_stride;
-                for (uint32_t i = tid; i < len; i += kBlock)
+                for (uint32_t i = tid; i < len; i += NT)
                     if (hrow[i] < a.vocab) hash_insert(s_hash, a.log2_slots, hrow[i]);
-                __syncthreads();
             }
+            __syncthreads();
             RowCtx full = ctx;
             full.bitmap = nullptr;
             uint2 *slots = s_big;  // 1024 entries of (float bits, id)
-            for (uint32_t L = tid; L < 1024u; L += kBlock) {
+            for (uint32_t L = tid; L < 1024u; L += NT) {
                 uint32_t bid = L;
                 float best = L < a.vocab ? configured_at<Elem>(full, L) : u2f(kLowestBits);
                 for (uint32_t t = L + 1024u; t < a.vocab; t += 1024u) {
-                    float c = configured_at<Elem>(full, t);
+                    const float c = configured_at<Elem>(full, t);
                     if (float_better(c, t, best, bid)) {
                         best = c;
                         bid = t;
@@ -685,8 +526,8 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             }
             __syncthreads();
             for (uint32_t stride = 512u; stride > 0u; stride >>= 1) {
-                for (uint32_t L = tid; L < stride; L += kBlock) {
-                    uint2 c = slots[L + stride], b = slots[L];
+                for (uint32_t L = tid; L < stride; L += NT) {
+                    const uint2 c = slots[L + stride], b = slots[L];
                     if (float_better(u2f(c.x), c.y, u2f(b.x), b.y)) slots[L] = c;
                 }
                 __syncthreads();
@@ -694,8 +535,9 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             token = slots[0].y;
             sel_bits = slots[0].x;
         } else {
-            uint2 e = s_sorted[0];
+            const uint2 e = s_sorted[0];
             if (e.x == kNegInfKey && a.vocab < 1024u) {
+                // every token is -inf: the shader's padded lane V (LOWEST_FLOAT) wins
                 token = a.vocab;
                 sel_bits = kLowestBits;
             } else {
@@ -703,13 +545,10 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
                 sel_bits = f2u(entry_value(e));
             }
         }
-        out_flags = 0u;
-        kout = 1;
         __syncthreads();
         if (tid == 0) s_p[0] = 1.0f;
     } else {
-        // pad to k with (LOWEST_FLOAT, 0xffffffff)
-        for (uint32_t i = n + tid; i < k; i += kBlock) s_sorted[i] = make_uint2(kMinFiniteKey, kPadId);
+        for (uint32_t i = n + tid; i < k; i += NT) s_sorted[i] = make_uint2(kMinFiniteKey, kPadId);
         __syncthreads();
         if (tid < 64) {
             const uint32_t lane = tid;
@@ -722,25 +561,24 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
                 const float d = T * lg;
                 minimum = l0 + d;
             }
-            // n_valid: leading survivors not below the min-p floor
+            // leading survivors not below the min-p floor
             uint32_t n_valid = k;
             for (uint32_t c0 = 0; c0 < k; c0 += 64u) {
                 const uint32_t i = c0 + lane;
-                const bool below = i < k && entry_value(s_sorted[i]) < minimum;
-                const uint64_t b = __ballot(below);
+                const uint64_t b = __ballot(i < k && entry_value(s_sorted[i]) < minimum);
                 if (b) {
                     n_valid = c0 + (uint32_t)__builtin_ctzll(b);
                     break;
                 }
             }
-            // weights and their sequential running sums (the reference's loop order)
+            // weights in parallel, running sums in the reference's sequential order
             float acc = 0.0f;
             for (uint32_t c0 = 0; c0 < n_valid; c0 += 64u) {
                 const uint32_t i = c0 + lane;
                 float w = 0.0f;
                 if (i < n_valid) {
-                    const float s = entry_value(s_sorted[i]) / T;
-                    w = nerve_expf(s - m);
+                    const float sc_ = entry_value(s_sorted[i]) / T;
+                    w = nerve_expf(sc_ - m);
                     s_w[i] = w;
                 }
                 const uint32_t cnt = min(64u, n_valid - c0);
@@ -752,7 +590,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
                 }
                 if (i < n_valid) s_p[i] = mine;
             }
-            const float total = n_valid ? s_p[n_valid - 1] : 0.0f;
+            const float total = n_valid ? s_p[n_valid - 1u] : 0.0f;
             const float threshold = P.top_p * total;
             uint32_t nucleus = n_valid;
             for (uint32_t c0 = 0; c0 < n_valid; c0 += 64u) {
@@ -766,7 +604,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             if (nucleus == 0u) nucleus = 1u;
             const float nucleus_weight = n_valid ? s_p[nucleus - 1u] : 0.0f;
             uint64_t tick;
-            uint32_t *sc = a.stream_control ? a.stream_control + (uint64_t)row * 5u : nullptr;
             if (sc) tick = (uint64_t)sc[1] | ((uint64_t)sc[2] << 32);
             else tick = a.steps ? a.steps[row] : 0ull;
             const uint32_t seed = a.seeds ? a.seeds[row] : 0u;
@@ -781,14 +618,10 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
                     break;
                 }
             }
-            // post-filter probabilities overwrite the running sums
-            for (uint32_t i = lane; i < k; i += 64u) {
-                const float pw = (i < nucleus && i < n_valid) ? s_w[i] / nucleus_weight : 0.0f;
-                s_p[i] = pw;
-            }
+            for (uint32_t i = lane; i < k; i += 64u) s_p[i] = (i < nucleus && i < n_valid) ? s_w[i] / nucleus_weight : 0.0f;
             if (lane == 0) {
                 const uint2 e = s_sorted[selected];
-                s_res[0] = e.y & kIdMask;
+                s_res[0] = e.y == kPadId ? kPadId : (e.y & kIdMask);
                 s_res[1] = f2u(entry_value(e));
             }
         }
@@ -800,7 +633,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     }
     __syncthreads();
 
-    // outputs
     if (tid == 0) {
         nerve_sampler_output o;
         o.token_id = token;
@@ -808,7 +640,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         o.flags = out_flags;
         o.reserved = 0u;
         a.out[row] = o;
-        uint32_t *sc = a.stream_control ? a.stream_control + (uint64_t)row * 5u : nullptr;
         if (sc) {
             const uint32_t lo = sc[1];
             if (a.ring) {
@@ -829,20 +660,17 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         }
     }
     if (a.topk_ids || a.topk_logits || a.topk_probs) {
-        for (uint32_t i = tid; i < a.kcap; i += kBlock) {
+        for (uint32_t i = tid; i < a.kcap; i += NT) {
             const uint64_t o = (uint64_t)row * a.kcap + i;
             const bool live = i < kout;
-            uint2 e = live ? s_sorted[i] : make_uint2(kMinFiniteKey, kPadId);
-            float value;
-            uint32_t id;
-            if (eos && i == 0) {
-                value = u2f(kLowestBits);
-                id = a.eos;
-            } else if (!sampled && !eos && i == 0) {
-                value = u2f(sel_bits);
+            float value = u2f(kLowestBits);
+            uint32_t id = kPadId;
+            if (live && i == 0 && (eos || !sampled)) {
+                value = eos ? u2f(kLowestBits) : u2f(sel_bits);
                 id = token;
-            } else {
-                value = live ? entry_value(e) : u2f(kLowestBits);
+            } else if (live) {
+                const uint2 e = s_sorted[i];
+                value = entry_value(e);
                 id = e.y == kPadId ? kPadId : (e.y & kIdMask);
             }
             if (a.topk_ids) a.topk_ids[o] = id;
@@ -850,6 +678,482 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             if (a.topk_probs) a.topk_probs[o] = live ? s_p[i] : 0.0f;
         }
     }
+}
+
+constexpr uint32_t kStages = 4;         // register ring depth of the slice stream
+constexpr uint32_t kStreamCandCap = 2048;
+
+// PEN: 0 = no penalty state, 1 = seen bitmap (set semantics), 2 = history ids (count semantics).
+// EPV elements per lane-vector, VPL lane-vectors per lane per stage.
+template <typename Elem, int EPV, int VPL, bool MASK, int PEN>
+__global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
+    constexpr int HPT = (kMaxHistory + kBlock - 1) / kBlock;  // history ids per lane
+    constexpr uint32_t CHV = (uint32_t)kBlock * VPL;           // lane-vectors per stage
+    constexpr bool history = PEN == 2;
+    using VT = VecTraits<Elem, EPV>;
+    using vec_t = typename VT::load_t;
+    __shared__ SharedSmall sm;
+    extern __shared__ __align__(16) uint32_t s_dyn[];
+    uint32_t *s_hash = s_dyn;                             // [hash_slots]
+    uint32_t *s_bitmap = s_hash + a.hash_slots;           // [bitmap_words]
+    uint2 *s_cand = (uint2 *)(s_bitmap + a.bitmap_words);  // [kStreamCandCap], later merge / top-p scratch
+    uint2 *s_sorted = s_cand + kStreamCandCap;            // [kcap]
+    uint2 *s_big = s_cand;
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = lane_id();
+    const uint32_t wave = tid >> 6;
+    const uint32_t logical = xcd_remap(blockIdx.x, gridDim.x);
+    const uint32_t row = logical / a.slices;
+    const uint32_t slice = logical % a.slices;
+
+    const nerve_sampler_row_params P = a.params[row];
+    const bool sampled = P.method != NERVE_METHOD_GREEDY;
+    uint32_t k = sampled ? P.top_k : 1u;
+    k = k < 1u ? 1u : (k > a.kcap ? a.kcap : k);
+    const uint32_t valid_min = sampled ? kMinFiniteKey : kNegInfKey;
+    const uint32_t masked_key = sampled ? 0u : kNegInfKey;
+
+    // The slice owns full EPV-element lane-vectors [v0, v1); the last slice
+    // also owns the V % EPV tail elements, one per lane.
+    const uint32_t nfull = a.nvec;
+    const uint32_t v0 = min(slice * a.vec_per_slice, nfull);
+    const uint32_t v1 = min(v0 + a.vec_per_slice, nfull);
+    const uint32_t nchunks = (v1 - v0 + CHV - 1u) / CHV;
+    const bool last_slice = slice == a.slices - 1u;
+    const uint32_t tok0 = v0 * EPV;
+    const uint32_t tok1 = last_slice ? a.vocab : v1 * EPV;
+    const uint32_t tail_id = nfull * EPV + tid;
+    const bool has_tail = last_slice && tail_id < a.vocab;
+
+    const Elem *lrow = (const Elem *)a.logits + (uint64_t)row * a.ld;
+    const uint32_t *arow = MASK ? a.allowed + (uint64_t)row * a.allowed_stride : nullptr;
+    const uint32_t *srow = PEN == 1 ? a.seen + (uint64_t)row * a.seen_stride : nullptr;
+    const uint32_t last_slot = nfull - 1u;
+
+    // Register ring of kStages stages; a stage is VPL lane-vectors per lane
+    // plus their mask / seen words. Addresses are clamped into the row, so the
+    // loads never branch and all stages of a lane stay in flight together.
+    vec_t ring[kStages][VPL];
+    uint32_t mring[kStages][VPL], sring[kStages][VPL];
+    auto issue = [&](uint32_t c, vec_t (&rv)[VPL], uint32_t (&mv)[VPL], uint32_t (&sv)[VPL]) {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            const uint32_t ls = min(v0 + c * CHV + (uint32_t)i * kBlock + tid, last_slot);
+            rv[i] = *(const vec_t *)(lrow + (uint64_t)ls * EPV);
+            if constexpr (MASK) mv[i] = arow[(ls * EPV) >> 5];
+            if constexpr (PEN == 1) sv[i] = srow[(ls * EPV) >> 5];
+        }
+    };
+
+    PHASE_MARK(0);
+    // 1. history ids, then the first kStages stages
+    uint32_t hist[history ? HPT : 1];
+    uint32_t hlen = 0;
+    if constexpr (history) {
+        const uint32_t *hrow = a.history + (uint64_t)row * a.history_stride;
+        const uint32_t hlast = a.history_stride - 1u;
+#pragma unroll
+        for (int h = 0; h < HPT; ++h) hist[h] = hrow[min(tid + (uint32_t)h * kBlock, hlast)];
+        hlen = min(a.history_len[row], a.history_stride);
+    }
+    const uint32_t tail_at = min(tail_id, a.vocab - 1u);
+    const uint32_t tail_bits = f2u(load_elem<Elem>(lrow, tail_at));
+    uint32_t tail_m = 0xffffffffu, tail_s = 0u;
+    if constexpr (MASK) tail_m = arow[tail_at >> 5];
+    if constexpr (PEN == 1) tail_s = srow[tail_at >> 5];
+    issue(0u, ring[0], mring[0], sring[0]);
+    issue(1u, ring[1], mring[1], sring[1]);
+    issue(2u, ring[2], mring[2], sring[2]);
+    issue(3u, ring[3], mring[3], sring[3]);
+
+    // 2. LDS state: counters, and the slice's history ids -> bitmap + hash
+    if constexpr (history) {
+        for (uint32_t i = tid; i < a.hash_slots; i += kBlock) s_hash[i] = kHashEmpty;
+        for (uint32_t i = tid; i < a.bitmap_words; i += kBlock) s_bitmap[i] = 0u;
+    }
+    if (tid == 0) sm.flag[1] = 0u;  // candidates appended
+    lds_sync();
+    if constexpr (history) {
+#pragma unroll
+        for (int h = 0; h < HPT; ++h) {
+            const uint32_t id = hist[h];
+            if (tid + (uint32_t)h * kBlock < hlen && id >= tok0 && id < tok1) {
+                const uint32_t o = id - tok0;
+                atomicOr(&s_bitmap[o >> 5], 1u << (o & 31u));
+                hash_insert(s_hash, a.log2_slots, id);
+            }
+        }
+        lds_sync();
+    }
+    PHASE_MARK(1);
+
+    // 3. stream the stages
+    uint32_t tmax = 0, best_id = kPadId;  // greedy: lane best; sampled: lane max so far
+    uint32_t any_allowed = 0, has_nan = 0;
+    uint32_t thr = 1u;                    // sampled: keys >= thr are kept (block-uniform)
+    auto take = [&](uint32_t key, uint32_t id) __attribute__((always_inline)) {
+        if (key > tmax || (key == tmax && key != 0u && id < best_id)) {
+            tmax = key;
+            best_id = id;
+        }
+    };
+    auto push = [&](uint32_t key, uint32_t id) __attribute__((always_inline)) {
+        const uint32_t pos = atomicAdd(&sm.flag[1], 1u);
+        if (pos < kStreamCandCap) s_cand[pos] = make_uint2(key, id);
+    };
+    // A token with penalty state competes with its configured value.
+    auto patch = [&](uint32_t bits, uint32_t id, uint32_t count) __attribute__((always_inline)) {
+        const float v = configured_logit(u2f(bits), true, count, P.repetition_penalty, P.frequency_penalty,
+                                         P.presence_penalty);
+        uint32_t key = order_key(v);
+        has_nan |= (v != v) ? 1u : 0u;
+        key = key < valid_min ? 0u : key;
+        if (!sampled) take(key, id);
+        else if (key >= thr && key != 0u) push(key, id);
+    };
+    // Penalties that never raise a logit (repetition >= 1, frequency and
+    // presence >= 0) cannot lift a token above a bound that its raw value does
+    // not reach, so tokens with penalty state need work only where their raw
+    // value passes; other settings patch every such token.
+    const bool lowering = P.repetition_penalty >= 1.0f && P.frequency_penalty >= 0.0f && P.presence_penalty >= 0.0f;
+
+    // Exact per-element work on one lane-vector. mode 0: per-lane maximum and
+    // flags (first pass over a sampled row's first stage); 1 and 2: append
+    // keys >= thr; 3: greedy per-lane best. In modes 1-3 an element whose raw
+    // key cannot pass is skipped before its configured value is computed.
+    auto exact_vec = [&](const vec_t &vec, uint32_t id0, uint32_t valid, uint32_t abits, uint32_t pbits, int mode) __attribute__((always_inline)) {
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) {
+            const uint32_t bits = VT::bits(vec, e);
+            const bool in = (valid >> e) & 1u, allowed = (abits >> e) & 1u, pen = (pbits >> e) & 1u;
+            if (mode == 0) any_allowed |= (in && allowed) ? 1u : 0u;
+            if (!in) continue;
+            if (mode != 0) {
+                const uint32_t raw_up = f32_key_upper(bits);
+                const bool can = mode == 3 ? (raw_up > tmax || tmax == 0u) : raw_up >= thr;
+                if (!can || (pen && !lowering)) continue;  // a raised value is patched separately
+            }
+            uint32_t key;
+            if (!allowed) {
+                key = masked_key;
+            } else if (pen) {
+                const uint32_t id = id0 + (uint32_t)e;
+                const uint32_t count = history ? hash_lookup(s_hash, a.log2_slots, id) : 1u;
+                const float v = configured_logit(u2f(bits), true, count, P.repetition_penalty, P.frequency_penalty,
+                                                 P.presence_penalty);
+                has_nan |= (v != v) ? 1u : 0u;
+                key = order_key(v);
+            } else {
+                has_nan |= ((bits & 0x7fffffffu) > 0x7f800000u) ? 1u : 0u;
+                key = raw_order_key(bits);
+            }
+            key = key < valid_min ? 0u : key;
+            if (mode == 0 || mode == 3) {
+                take(key, id0 + (uint32_t)e);
+            } else if (key >= thr && key != 0u) {
+                push(key, id0 + (uint32_t)e);
+            }
+        }
+    };
+    // Modes as above; modes 2 (later stages of sampled rows) and 3 (greedy)
+    // first take a packed-integer upper bound of the lane-vector's raw keys and
+    // run the exact code only where it can matter.
+    auto process = [&](uint32_t c, const vec_t (&rv)[VPL], const uint32_t (&mv)[VPL], const uint32_t (&sv)[VPL],
+                       int mode) {
+#ifdef NERVE_DEBUG_NOPROCESS
+        // profiling builds only: consume the ring without any selection work
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) tmax = max(tmax, VT::bits(rv[i], 0));
+        return;
+#endif
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            const uint32_t vi = (uint32_t)i * kBlock + tid;
+            const uint32_t slot = v0 + c * CHV + vi;
+            const uint32_t id0 = slot * EPV;
+            const vec_t vec = rv[i];
+            const uint32_t valid = slot < v1 ? ((1u << EPV) - 1u) : 0u;
+            uint32_t pbits = 0u;
+            if constexpr (history) pbits = valid ? s_bitmap[(id0 - tok0) >> 5] >> ((id0 - tok0) & 31u) : 0u;
+            if constexpr (PEN == 1) pbits = sv[i] >> (id0 & 31u);
+            uint32_t abits = 0xffffffffu;
+            if constexpr (MASK) abits = mv[i] >> (id0 & 31u);
+            pbits &= valid & abits;
+            if (mode <= 1) {
+                exact_vec(vec, id0, valid, abits, pbits, mode);
+            } else {
+                const uint32_t live = valid & abits;
+                any_allowed |= live ? 1u : 0u;
+                if (mode == 3) has_nan |= (valid && VT::has_nan(vec)) ? 1u : 0u;
+                bool go = false;
+                if (live) {
+                    const uint32_t up = VT::upper(vec);
+                    go = mode == 2 ? up >= thr : (up > tmax || tmax == 0u);
+                }
+                if (go) exact_vec(vec, id0, valid, abits, pbits, mode);
+#ifdef NERVE_PHASE_TIMING
+                {
+                    const uint64_t bw = __ballot(go);
+                    if (lane == 0u) {
+                        DBG_ADD(0, (uint32_t)__popcll(bw));
+                        DBG_ADD(1, bw ? 1u : 0u);
+                    }
+                }
+#endif
+            }
+            if (mode != 0 && !lowering) {
+                while (pbits) {
+                    const uint32_t e = (uint32_t)__builtin_ctz(pbits);
+                    pbits &= pbits - 1u;
+                    const uint32_t id = id0 + e;
+                    patch(VT::bits_dyn(vec, e), id, history ? hash_lookup(s_hash, a.log2_slots, id) : 1u);
+                }
+            }
+        }
+    };
+    // thr after the first stage: first 16 bits of the k-th largest per-lane
+    // maximum (at least k keys are >= it). Later refreshes: the exact k-th
+    // largest key among the candidates kept so far (every key >= the old thr
+    // is among them, so it is the running k-th largest). thr only rises.
+    auto first_threshold = [&]() __attribute__((always_inline)) {
+        uint32_t unused;
+        const uint32_t tm[1] = {tmax};
+        const uint32_t t = radix_threshold<1>(tm, k, 2, sm.hist, sm.sel, unused);
+        thr = t > thr ? t : thr;
+    };
+    auto refresh_threshold = [&]() __attribute__((always_inline)) {
+        lds_sync();
+        const uint32_t C = sm.flag[1];
+        if (C >= k && C <= kStreamCandCap) {
+            auto cand_key = [&](uint32_t i) __attribute__((always_inline)) -> uint32_t { return s_cand[i].x; };
+            uint32_t unused;
+            const uint32_t t = radix_threshold_fn(0u, C, k, sm.hist, sm.sel, unused, cand_key);
+            thr = t > thr ? t : thr;
+        }
+    };
+
+    // One ring slot per call, addressed at compile time: the processing of
+    // stage c overlaps the loads of stages c+1 .. c+3, and the refill of the
+    // slot is issued unconditionally (addresses past the slice clamp to the
+    // last slot and are masked out), so every path has the same loads in
+    // flight and the compiler waits only for the slot about to be used.
+    auto stage = [&](uint32_t c, vec_t (&rv)[VPL], uint32_t (&mv)[VPL], uint32_t (&sv)[VPL], bool may_be_first) {
+        if (c < nchunks) {
+            if (!sampled) {
+                process(c, rv, mv, sv, 3);
+            } else if (may_be_first && c == 0u) {
+                process(0u, rv, mv, sv, 0);
+                first_threshold();
+                process(0u, rv, mv, sv, 1);
+            } else {
+                process(c, rv, mv, sv, 2);
+                if (c == 1u || c == 3u || c == 7u || c == 15u) refresh_threshold();
+            }
+        }
+        issue(c + kStages, rv, mv, sv);
+    };
+    for (uint32_t c0 = 0; c0 < nchunks; c0 += kStages) {
+        stage(c0 + 0u, ring[0], mring[0], sring[0], true);
+        stage(c0 + 1u, ring[1], mring[1], sring[1], false);
+        stage(c0 + 2u, ring[2], mring[2], sring[2], false);
+        stage(c0 + 3u, ring[3], mring[3], sring[3], false);
+    }
+    PHASE_MARK(2);
+
+    // the tail elements of the last slice
+    if (has_tail) {
+        bool allowed = true;
+        if constexpr (MASK) allowed = (tail_m >> (tail_at & 31u)) & 1u;
+        uint32_t pbit = 0u;
+        if constexpr (history) {
+            const uint32_t o = tail_id - tok0;
+            pbit = (s_bitmap[o >> 5] >> (o & 31u)) & 1u;
+        }
+        if constexpr (PEN == 1) pbit = (tail_s >> (tail_at & 31u)) & 1u;
+        any_allowed |= allowed ? 1u : 0u;
+        has_nan |= (allowed && (tail_bits & 0x7fffffffu) > 0x7f800000u) ? 1u : 0u;
+        if (pbit && allowed) {
+            patch(tail_bits, tail_id, history ? hash_lookup(s_hash, a.log2_slots, tail_id) : 1u);
+        } else {
+            uint32_t key = allowed ? raw_order_key(tail_bits) : masked_key;
+            key = key < valid_min ? 0u : key;
+            take(key, tail_id);
+            if (sampled && key >= thr && key != 0u) push(key, tail_id);
+        }
+    }
+
+    RowCtx ctx;
+    ctx.logits_row = lrow;
+    ctx.allowed_row = arow;
+    ctx.seen_row = srow;
+    ctx.hash = s_hash;
+    ctx.bitmap = s_bitmap;
+    ctx.log2_slots = a.log2_slots;
+    ctx.tok0 = tok0;
+    ctx.rep = P.repetition_penalty;
+    ctx.freq = P.frequency_penalty;
+    ctx.pres = P.presence_penalty;
+    ctx.history = history;
+
+    // slice flags: bit 0 = some token allowed, bit 1 = some configured value is NaN
+    const uint32_t fsum = block_sum(any_allowed | (has_nan << 16), sm.scan);
+    const uint32_t flags_slice = ((fsum & 0xffffu) ? 1u : 0u) | ((fsum >> 16) ? 2u : 0u);
+    PHASE_MARK(3);
+
+    // 4. selection -> s_sorted[0 .. n_out)
+    uint32_t n_out = 0;
+    if (!sampled) {
+        const uint64_t packed = tmax ? (((uint64_t)tmax << 32) | (uint64_t)(~best_id)) : 0ull;
+        const uint64_t m = block_max_u64(packed, sm.red);
+        if (m != 0ull) {
+            if (tid == 0) s_sorted[0] = make_uint2((uint32_t)(m >> 32), ~(uint32_t)m);
+            n_out = 1;
+        }
+        lds_sync();
+    } else {
+        uint32_t C = sm.flag[1];
+        PHASE_MARK(4);
+        if (tid == 0) {
+            DBG_SET(2, C);
+            DBG_SET(3, thr);
+        }
+        if (C > kStreamCandCap) {
+            // Skewed slice: exact selection recomputed from memory (rare). The
+            // k-th largest key kv, then the `need` smallest ids among keys == kv.
+            auto key_at = [&](uint32_t tt) __attribute__((always_inline)) -> uint32_t {
+                const uint32_t key = order_key(configured_at<Elem>(ctx, tt));
+                return key < valid_min ? 0u : key;
+            };
+            uint32_t count_ge;
+            const uint32_t kv = radix_threshold_fn(tok0, tok1, k, sm.hist, sm.sel, count_ge, key_at);
+            uint32_t gt = 0;
+            for (uint32_t tt = tok0 + tid; tt < tok1; tt += kBlock) gt += key_at(tt) > kv ? 1u : 0u;
+            const uint32_t G = block_sum(gt, sm.scan);
+            const uint32_t need = k - G;
+            auto tie_at = [&](uint32_t tt) __attribute__((always_inline)) -> uint32_t { return key_at(tt) == kv ? ~tt : 0u; };
+            uint32_t ties_ge;
+            const uint32_t id_cut = ~radix_threshold_fn(tok0, tok1, need, sm.hist, sm.sel, ties_ge, tie_at);
+            if (tid == 0) sm.flag[1] = 0u;
+            lds_sync();
+            for (uint32_t tt = tok0 + tid; tt < tok1; tt += kBlock) {
+                const uint32_t key = key_at(tt);
+                if (key > kv || (key == kv && tt <= id_cut)) {
+                    const uint32_t q = atomicAdd(&sm.flag[1], 1u);
+                    if (q < kStreamCandCap) s_cand[q] = make_uint2(key, tt);
+                }
+            }
+            lds_sync();
+            C = min(sm.flag[1], kStreamCandCap);
+        }
+        // rank sort (ids are distinct, so ranks are a permutation)
+        for (uint32_t i = tid; i < C; i += kBlock) {
+            const uint2 e = s_cand[i];
+            uint32_t r0 = 0, r1 = 0, r2 = 0, r3 = 0;
+            uint32_t j = 0;
+            for (; j + 4u <= C; j += 4u) {
+                r0 += entry_better(s_cand[j], e) ? 1u : 0u;
+                r1 += entry_better(s_cand[j + 1u], e) ? 1u : 0u;
+                r2 += entry_better(s_cand[j + 2u], e) ? 1u : 0u;
+                r3 += entry_better(s_cand[j + 3u], e) ? 1u : 0u;
+            }
+            for (; j < C; ++j) r0 += entry_better(s_cand[j], e) ? 1u : 0u;
+            const uint32_t r = r0 + r1 + r2 + r3;
+            if (r < k) s_sorted[r] = e;
+        }
+        n_out = C < k ? C : k;
+        lds_sync();
+    }
+    PHASE_MARK(5);
+
+    // the sign of a zero survivor comes from its own configured value
+    for (uint32_t i = tid; i < n_out; i += kBlock) {
+        const uint2 e = s_sorted[i];
+        if (e.x == kZeroKey) {
+            const float v = configured_at<Elem>(ctx, e.y);
+            if (f2u(v) == 0x80000000u) s_sorted[i].y = e.y | kNegZeroFlag;
+        }
+    }
+    __syncthreads();
+    PHASE_MARK(6);
+
+    // 5. publish: with several slices the sorted list goes to scratch and the
+    // finish kernel merges the row; a single slice finishes here.
+    if (a.slices > 1) {
+        uint2 *lists = a.scratch_lists + (uint64_t)(row * a.slices + slice) * a.kcap;
+        for (uint32_t i = tid; i < n_out; i += kBlock) lists[i] = s_sorted[i];
+        if (tid == 0) a.scratch_meta[row * a.slices + slice] = n_out | (flags_slice << 16);
+        PHASE_MARK(7);
+        return;
+    }
+    finish_row<Elem, PEN, kBlock>(a, row, P, k, sampled, n_out, flags_slice, s_sorted, s_big, s_hash, ctx);
+}
+
+// Merges the S sorted slice lists of each row (one workgroup per row) and
+// finishes the row. Launched after sample_rows_kernel on the same stream, so
+// the slice lists are visible without any cross-workgroup fence.
+template <typename Elem, int PEN>
+__global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
+    extern __shared__ uint32_t s_dyn[];
+    uint32_t *s_hash = s_dyn;
+    uint2 *s_big = (uint2 *)(s_dyn + a.hash_slots);
+    uint2 *s_sorted = s_big + a.big_entries;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t row = blockIdx.x;
+    const nerve_sampler_row_params P = a.params[row];
+    const bool sampled = P.method != NERVE_METHOD_GREEDY;
+    uint32_t k = sampled ? P.top_k : 1u;
+    k = k < 1u ? 1u : (k > a.kcap ? a.kcap : k);
+
+    const uint2 *all = a.scratch_lists + (uint64_t)row * a.slices * a.kcap;
+    const uint32_t *meta = a.scratch_meta + row * a.slices;
+    uint32_t total = 0, row_flags = 0;
+    for (uint32_t s = 0; s < a.slices; ++s) {
+        const uint32_t m = meta[s];
+        total += m & 0xffffu;
+        row_flags |= m >> 16;
+    }
+    const uint32_t ne = a.slices * a.kcap;
+    for (uint32_t i = tid; i < ne; i += kFinishBlock) {
+        const uint32_t s = i / a.kcap, pos = i % a.kcap;
+        if (pos < (meta[s] & 0xffffu)) s_big[i] = all[i];
+    }
+    __syncthreads();
+    // rank of an entry = its position in its own sorted list plus the number
+    // of better entries in every other list (binary search); ids are distinct
+    for (uint32_t i = tid; i < ne; i += kFinishBlock) {
+        const uint32_t s = i / a.kcap, pos = i % a.kcap;
+        if (pos >= (meta[s] & 0xffffu)) continue;
+        const uint2 e = s_big[i];
+        uint32_t r = pos;
+        for (uint32_t o = 0; o < a.slices && r < k; ++o) {
+            if (o == s) continue;
+            const uint2 *lo = s_big + o * a.kcap;
+            uint32_t lo_i = 0, hi_i = meta[o] & 0xffffu;
+            while (lo_i < hi_i) {
+                const uint32_t mid = (lo_i + hi_i) >> 1;
+                if (entry_better(lo[mid], e)) lo_i = mid + 1; else hi_i = mid;
+            }
+            r += lo_i;
+        }
+        if (r < k) s_sorted[r] = e;
+    }
+    const uint32_t n = total < k ? total : k;
+    __syncthreads();
+
+    RowCtx ctx;
+    ctx.logits_row = (const Elem *)a.logits + (uint64_t)row * a.ld;
+    ctx.allowed_row = a.allowed ? a.allowed + (uint64_t)row * a.allowed_stride : nullptr;
+    ctx.seen_row = PEN == 1 ? a.seen + (uint64_t)row * a.seen_stride : nullptr;
+    ctx.hash = s_hash;
+    ctx.bitmap = nullptr;
+    ctx.log2_slots = a.log2_slots;
+    ctx.tok0 = 0;
+    ctx.rep = P.repetition_penalty;
+    ctx.freq = P.frequency_penalty;
+    ctx.pres = P.presence_penalty;
+    ctx.history = PEN == 2;
+    finish_row<Elem, PEN, kFinishBlock>(a, row, P, k, sampled, n, row_flags, s_sorted, s_big, s_hash, ctx);
 }
 
 __global__ void record_tokens_kernel(uint32_t *seen, uint32_t seen_stride, uint32_t rows, const uint32_t *ids,
@@ -869,38 +1173,39 @@ __global__ void record_tokens_kernel(uint32_t *seen, uint32_t seen_stride, uint3
 
 // ---- launch ------------------------------------------------------------------
 
-template <typename Elem, int EPV, int NV, bool MASK, int PEN>
-static hipError_t launch_one(const StepArgs &a, hipStream_t stream) {
-    const size_t dyn = a.dyn_lds_bytes;
-    auto kern = sample_rows_kernel<Elem, EPV, NV, MASK, PEN>;
-    if (dyn > 48u * 1024u) {
-        hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn);
+template <typename Elem, int EPV, int VPL, bool MASK, int PEN>
+static hipError_t launch_one(const StepArgs &a0, hipStream_t stream) {
+    StepArgs a = a0;
+    a.dyn_lds_bytes = a.hash_slots * 4u + a.bitmap_words * 4u + kStreamCandCap * 8u + a.kcap * 8u;
+    auto kern = sample_rows_kernel<Elem, EPV, VPL, MASK, PEN>;
+    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)a.dyn_lds_bytes);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(a.batch * a.slices), dim3(kBlock), a.dyn_lds_bytes, stream, a);
+    e = hipGetLastError();
+    if (e != hipSuccess || a.slices == 1u) return e;
+    auto fin = finish_rows_kernel<Elem, PEN>;
+    if (a.finish_lds_bytes > 48u * 1024u) {
+        e = hipFuncSetAttribute((const void *)fin, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)a.finish_lds_bytes);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(kern, dim3(a.batch * a.slices), dim3(kBlock), dyn, stream, a);
+    hipLaunchKernelGGL(fin, dim3(a.batch), dim3(kFinishBlock), a.finish_lds_bytes, stream, a);
     return hipGetLastError();
 }
 
-template <typename Elem, int EPV, int NV>
+template <typename Elem, int EPV, int VPL>
 static hipError_t launch_variant(const StepArgs &a, hipStream_t stream) {
     const bool mask = a.allowed != nullptr;
     const int pen = a.history ? 2 : (a.seen ? 1 : 0);
     if (mask) {
-        if (pen == 2) return launch_one<Elem, EPV, NV, true, 2>(a, stream);
-        if (pen == 1) return launch_one<Elem, EPV, NV, true, 1>(a, stream);
-        return launch_one<Elem, EPV, NV, true, 0>(a, stream);
+        if (pen == 2) return launch_one<Elem, EPV, VPL, true, 2>(a, stream);
+        if (pen == 1) return launch_one<Elem, EPV, VPL, true, 1>(a, stream);
+        return launch_one<Elem, EPV, VPL, true, 0>(a, stream);
     }
-    if (pen == 2) return launch_one<Elem, EPV, NV, false, 2>(a, stream);
-    if (pen == 1) return launch_one<Elem, EPV, NV, false, 1>(a, stream);
-    return launch_one<Elem, EPV, NV, false, 0>(a, stream);
-}
-
-uint32_t elems_per_thread(uint32_t variant) {
-    switch (variant) {
-        case kVariantF32Vec: return 4u * 8u;
-        case kVariantBf16Vec: return 8u * 8u;
-        default: return 16u;
-    }
+    if (pen == 2) return launch_one<Elem, EPV, VPL, false, 2>(a, stream);
+    if (pen == 1) return launch_one<Elem, EPV, VPL, false, 1>(a, stream);
+    return launch_one<Elem, EPV, VPL, false, 0>(a, stream);
 }
 
 uint32_t elems_per_vector(uint32_t variant) {
@@ -912,14 +1217,20 @@ uint32_t elems_per_vector(uint32_t variant) {
 }
 
 uint32_t block_threads() { return (uint32_t)kBlock; }
-uint32_t cand_capacity() { return kCandCap; }
+uint32_t merge_capacity() { return kCandCap; }
+
+// LDS use of the slice kernel (hash, bitmap, candidates, sorted list); the
+// launch computes the same sum.
+uint32_t stream_lds_bytes(uint32_t, bool, bool, uint32_t hash_slots, uint32_t bitmap_words, uint32_t kcap) {
+    return hash_slots * 4u + bitmap_words * 4u + kStreamCandCap * 8u + kcap * 8u;
+}
 
 hipError_t launch_sample_rows(uint32_t variant, const StepArgs &a, hipStream_t stream) {
     switch (variant) {
-        case kVariantF32Vec: return launch_variant<float, 4, 8>(a, stream);
-        case kVariantBf16Vec: return launch_variant<uint16_t, 8, 8>(a, stream);
-        case kVariantF32Scalar: return launch_variant<float, 1, 16>(a, stream);
-        case kVariantBf16Scalar: return launch_variant<uint16_t, 1, 16>(a, stream);
+        case kVariantF32Vec: return launch_variant<float, 4, 2>(a, stream);
+        case kVariantBf16Vec: return launch_variant<uint16_t, 8, 2>(a, stream);
+        case kVariantF32Scalar: return launch_variant<float, 1, 4>(a, stream);
+        case kVariantBf16Scalar: return launch_variant<uint16_t, 1, 4>(a, stream);
         default: return hipErrorInvalidValue;
     }
 }
@@ -933,3 +1244,16 @@ hipError_t launch_record_tokens(uint32_t *seen, uint32_t seen_stride, uint32_t r
 }
 
 }  // namespace nerve
+
+#ifdef NERVE_PHASE_TIMING
+extern "C" int nerve_debug_phase_ts(uint64_t *host, size_t count) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(nerve::g_phase_ts), count * sizeof(uint64_t));
+}
+extern "C" int nerve_debug_counters(uint32_t *host, size_t count) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(nerve::g_dbg), count * sizeof(uint32_t));
+}
+extern "C" int nerve_debug_clear(void) {
+    static uint32_t zeros[16384 * 4];
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(nerve::g_dbg), zeros, sizeof(zeros));
+}
+#endif
