@@ -193,8 +193,9 @@ int nerve_sampler_create(const nerve_sampler_desc *desc, nerve_sampler **out) {
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(NERVE_ERR_HIP, std::string("the sampler kernels are built for gfx950 only, device is ") + prop.gcnArchName);
 
-    // Workgroups per row: one streams a whole row in stages; small batches
-    // split rows so the launch still covers the CUs (one workgroup per CU).
+    // Workgroups per row: a workgroup holds its slice of the row in VGPRs, so
+    // a slice is at most block_threads() * max_vectors_per_lane() lane-vectors;
+    // small batches split rows further so the launch still covers the CUs.
     const uint32_t threads = nerve::block_threads();
     uint32_t want = d.slices_per_row;
     if (want == 0u) {
@@ -203,11 +204,12 @@ int nerve_sampler_create(const nerve_sampler_desc *desc, nerve_sampler **out) {
         const uint32_t by_size = d.vocab_size / (threads * 16u);  // keep >= 16 elements per lane
         if (want > by_size) want = by_size;
         if (want > 64u) want = 64u;
-        const uint32_t by_merge = 12288u / d.top_k_capacity;  // merge area of the finish kernel
-        if (want > by_merge) want = by_merge;
         if (want == 0u) want = 1u;
     }
-    const uint32_t capacity = want;
+    // The one-element-per-load kernels hold the fewest tokens per slice.
+    const uint32_t scalar_tokens = threads * nerve::max_vectors_per_lane(nerve::kVariantF32Scalar);
+    const uint32_t need = (d.vocab_size + scalar_tokens - 1u) / scalar_tokens;
+    const uint32_t capacity = want > need ? want : need;
     if ((uint64_t)capacity * d.top_k_capacity > 12288u)
         return fail(NERVE_ERR_INVALID_SAMPLING_SPEC, "slices_per_row * top_k_capacity exceeds the 12288-entry merge area");
 
@@ -280,8 +282,14 @@ int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *str
 
     const uint32_t epv = nerve::elems_per_vector(variant);
     const uint32_t nvec = d.vocab_size / epv;  // full slots; the V % epv tail goes to the last slice
-    const uint32_t slices = s->slices;
+    const uint32_t per_slice_max = nerve::block_threads() * nerve::max_vectors_per_lane(variant);
+    uint32_t slices = s->slices;
+    const uint32_t slices_need = (nvec + per_slice_max - 1u) / per_slice_max;
+    if (slices < slices_need) slices = slices_need;
+    if (slices > s->slices_capacity) return fail(NERVE_ERR_INVALID_ARGUMENT, "vocabulary needs more slices than the scratch holds");
     const uint32_t vec_per_slice = (nvec + slices - 1u) / slices;
+    const uint32_t nv = nerve::vectors_per_lane(variant, (vec_per_slice + nerve::block_threads() - 1u) / nerve::block_threads());
+    if (nv == 0u) return fail(NERVE_ERR_INVALID_ARGUMENT, "slice exceeds the kernel's register capacity");
 
     nerve::StepArgs a;
     std::memset(&a, 0, sizeof(a));
@@ -314,21 +322,21 @@ int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *str
     a.eos = b->eos_token_id;
     a.nvec = nvec;
     a.vec_per_slice = vec_per_slice;
+    a.nv = nv;
     if (b->history) {
         a.hash_slots = next_pow2(2u * b->history_stride);
         if (a.hash_slots < 64u) a.hash_slots = 64u;
         a.log2_slots = log2u(a.hash_slots);
     }
-    if (b->history) {
-        const uint32_t slice_tokens = vec_per_slice * epv + epv;
-        a.bitmap_words = ((slice_tokens + 31u) / 32u + 3u) & ~1u;
-    }
+    const bool pen = b->history != nullptr || b->seen != nullptr;
+    if (pen || b->allowed) a.bitmap_words = nerve::bitmap_words_for(variant, vec_per_slice);
     uint32_t big = nerve::merge_capacity();
     if (slices * d.top_k_capacity > big) big = slices * d.top_k_capacity;
     a.big_entries = big;
     a.finish_lds_bytes = a.hash_slots * 4u + big * 8u + d.top_k_capacity * 8u;
-    const uint32_t stream_lds = nerve::stream_lds_bytes(variant, b->allowed != nullptr, b->seen != nullptr,
-                                                        a.hash_slots, a.bitmap_words, d.top_k_capacity);
+    const uint32_t stream_lds = nerve::stream_lds_bytes(variant, b->allowed != nullptr, pen, a.hash_slots,
+                                                        a.bitmap_words, d.top_k_capacity);
+    a.dyn_lds_bytes = stream_lds;
     const size_t static_lds = 2u * 1024u;  // reduction scratch
     if (stream_lds + static_lds > s->lds_per_block || a.finish_lds_bytes + static_lds > s->lds_per_block)
         return fail(NERVE_ERR_INVALID_ARGUMENT, "LDS need of this top_k_capacity / history / slice count exceeds the device");

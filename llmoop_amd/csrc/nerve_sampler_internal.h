@@ -44,10 +44,11 @@ struct StepArgs {
     uint32_t rng;
     uint32_t eos;
     uint32_t nvec;           // full vector slots per row (vocab / elements per slot)
-    uint32_t vec_per_slice;
+    uint32_t vec_per_slice;  // <= kBlock * nv
+    uint32_t nv;             // lane-vectors per lane of the launched kernel
     uint32_t hash_slots;     // power of two, 0 without a history
     uint32_t log2_slots;
-    uint32_t bitmap_words;   // LDS words of the slice's history bitmap (even; 0 without a history)
+    uint32_t bitmap_words;   // LDS words of each slice bitmap (penalty state, mask)
     uint32_t big_entries;    // uint2 entries of the candidate / merge area
     uint32_t dyn_lds_bytes;     // slice kernel
     uint32_t finish_lds_bytes;  // finish kernel (slices > 1)
@@ -56,8 +57,11 @@ struct StepArgs {
 uint32_t elems_per_vector(uint32_t variant);
 uint32_t block_threads();
 uint32_t merge_capacity();
-uint32_t stream_lds_bytes(uint32_t variant, bool mask, bool seen, uint32_t hash_slots, uint32_t bitmap_words,
+uint32_t stream_lds_bytes(uint32_t variant, bool mask, bool pen, uint32_t hash_slots, uint32_t bitmap_words,
                           uint32_t kcap);
+uint32_t max_vectors_per_lane(uint32_t variant);
+uint32_t vectors_per_lane(uint32_t variant, uint32_t need);  // 0 when need exceeds every kernel
+uint32_t bitmap_words_for(uint32_t variant, uint32_t vec_per_slice);
 hipError_t launch_sample_rows(uint32_t variant, const StepArgs &a, hipStream_t stream);
 hipError_t launch_record_tokens(uint32_t *seen, uint32_t seen_stride, uint32_t rows, const uint32_t *ids,
                                 uint32_t ids_stride, const uint32_t *counts, uint32_t max_count, uint32_t vocab,

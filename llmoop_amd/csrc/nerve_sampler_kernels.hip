@@ -230,9 +230,29 @@ __device__ __forceinline__ uint32_t f32_key_upper(uint32_t w) {
     const uint32_t key = w ^ ((uint32_t)((int32_t)w >> 31) | 0x80000000u);
     return key == 0x7fffffffu ? 0x80000000u : key;
 }
+__device__ __forceinline__ uint32_t i32_max(uint32_t a, uint32_t b) { return (uint32_t)max((int32_t)a, (int32_t)b); }
+
+__device__ __forceinline__ uint32_t i16x2_max(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(i16x2, a), __builtin_bit_cast(i16x2, b)));
+}
+
+// Raw-bit maxima. Read as signed integers, the bit patterns of non-negative
+// values order like the values and sit above every negative one, so the
+// signed maximum of a set is its largest value whenever that is >= +0 (and
+// otherwise still one of its elements). vmax() reduces one lane-vector into
+// the accumulator form (packed i16 pairs for bf16, one i32 for f32); merge()
+// folds two accumulators; report_bits() gives the binary32 pattern of report r
+// (0x80000000, the bits of -0.0, is the empty marker); ge_pos(vm, thr) tests
+// whether a vmax() value holds a key >= thr, valid when thr > kZeroKey.
 template <>
 struct VecTraits<float, 4> {
     using load_t = u32x4;
+    static constexpr int kReports = 1;
+    static constexpr uint32_t kAccInit = 0x80000000u;
+    __device__ static __forceinline__ uint32_t vmax(const load_t &r) { return i32_max(i32_max(r[0], r[1]), i32_max(r[2], r[3])); }
+    __device__ static __forceinline__ uint32_t merge(uint32_t a, uint32_t b) { return i32_max(a, b); }
+    __device__ static __forceinline__ uint32_t report_bits(uint32_t acc, int) { return acc; }
+    __device__ static __forceinline__ bool ge_pos(uint32_t vm, uint32_t thr) { return (int32_t)vm >= (int32_t)(thr & 0x7fffffffu); }
     __device__ static __forceinline__ uint32_t upper(const load_t &r) {
         const uint32_t a = max(f32_key_upper(r[0]), f32_key_upper(r[1]));
         const uint32_t b = max(f32_key_upper(r[2]), f32_key_upper(r[3]));
@@ -252,6 +272,15 @@ struct VecTraits<float, 4> {
 template <>
 struct VecTraits<uint16_t, 8> {
     using load_t = u32x4;
+    static constexpr int kReports = 2;
+    static constexpr uint32_t kAccInit = 0x80008000u;
+    __device__ static __forceinline__ uint32_t vmax(const load_t &r) { return i16x2_max(i16x2_max(r[0], r[1]), i16x2_max(r[2], r[3])); }
+    __device__ static __forceinline__ uint32_t merge(uint32_t a, uint32_t b) { return i16x2_max(a, b); }
+    __device__ static __forceinline__ uint32_t report_bits(uint32_t acc, int r) { return r == 0 ? acc << 16 : acc & 0xffff0000u; }
+    __device__ static __forceinline__ bool ge_pos(uint32_t vm, uint32_t thr) {
+        const int32_t m = max((int32_t)(int16_t)(vm & 0xffffu), (int32_t)(int16_t)(vm >> 16));
+        return m >= (int32_t)(((thr & 0x7fffffffu) + 0xffffu) >> 16);
+    }
     __device__ static __forceinline__ uint32_t upper(const load_t &r) {
         const uint32_t m2 = u16x2_max(u16x2_max(bf16x2_keys(r[0]), bf16x2_keys(r[1])),
                                       u16x2_max(bf16x2_keys(r[2]), bf16x2_keys(r[3])));
@@ -277,6 +306,12 @@ struct VecTraits<uint16_t, 8> {
 template <>
 struct VecTraits<float, 1> {
     using load_t = float;
+    static constexpr int kReports = 1;
+    static constexpr uint32_t kAccInit = 0x80000000u;
+    __device__ static __forceinline__ uint32_t vmax(const load_t &r) { return f2u(r); }
+    __device__ static __forceinline__ uint32_t merge(uint32_t a, uint32_t b) { return i32_max(a, b); }
+    __device__ static __forceinline__ uint32_t report_bits(uint32_t acc, int) { return acc; }
+    __device__ static __forceinline__ bool ge_pos(uint32_t vm, uint32_t thr) { return (int32_t)vm >= (int32_t)(thr & 0x7fffffffu); }
     __device__ static __forceinline__ uint32_t upper(const load_t &r) { return f32_key_upper(f2u(r)); }
     __device__ static __forceinline__ bool has_nan(const load_t &r) { return (f2u(r) & 0x7fffffffu) > 0x7f800000u; }
     __device__ static __forceinline__ uint32_t bits(const load_t &r, int) { return f2u(r); }
@@ -286,6 +321,12 @@ struct VecTraits<float, 1> {
 template <>
 struct VecTraits<uint16_t, 1> {
     using load_t = uint16_t;
+    static constexpr int kReports = 1;
+    static constexpr uint32_t kAccInit = 0x80000000u;
+    __device__ static __forceinline__ uint32_t vmax(const load_t &r) { return (uint32_t)r << 16; }
+    __device__ static __forceinline__ uint32_t merge(uint32_t a, uint32_t b) { return i32_max(a, b); }
+    __device__ static __forceinline__ uint32_t report_bits(uint32_t acc, int) { return acc; }
+    __device__ static __forceinline__ bool ge_pos(uint32_t vm, uint32_t thr) { return (int32_t)vm >= (int32_t)(thr & 0x7fffffffu); }
     __device__ static __forceinline__ uint32_t upper(const load_t &r) { return f32_key_upper((uint32_t)r << 16); }
     __device__ static __forceinline__ bool has_nan(const load_t &r) { return ((uint32_t)r & 0x7fffu) > 0x7f80u; }
     __device__ static __forceinline__ uint32_t bits(const load_t &r, int) { return (uint32_t)r << 16; }
@@ -461,6 +502,7 @@ struct SharedSmall {
     uint32_t scan[kWaves];
     uint64_t red[kWaves];
     uint32_t flag[4];
+    uint32_t ones[1];  // all-ones mask word of rows without a mask
 };
 
 __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t n) {
@@ -680,29 +722,55 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
     }
 }
 
-constexpr uint32_t kStages = 4;         // register ring depth of the slice stream
-constexpr uint32_t kStreamCandCap = 2048;
+constexpr uint32_t kStageCap = 1024;       // lane-vectors staged for exact work per slice
+constexpr uint32_t kStreamCandCap = 2048;  // candidate entries per slice
 
-// PEN: 0 = no penalty state, 1 = seen bitmap (set semantics), 2 = history ids (count semantics).
-// EPV elements per lane-vector, VPL lane-vectors per lane per stage.
-template <typename Elem, int EPV, int VPL, bool MASK, int PEN>
+// Bitmap words of a slice: its tokens [tok0, tok1) rounded out to 32-token
+// words, plus slack; the host sizes the LDS bitmaps with the same bound.
+__host__ __device__ constexpr uint32_t slice_bitmap_words(uint32_t tokens, uint32_t epv) {
+    return (tokens + epv + 62u) / 32u + 1u;
+}
+
+// PEN: 0 = no penalty state, 1 = seen bitmap (set semantics), 2 = history ids
+// (count semantics). EPV elements per lane-vector, NV lane-vectors per lane.
+//
+// The slice [v0, v1) of full lane-vectors lives in VGPRs: wave w owns slots
+// v0 + w * 64 * NV + [0, 64 * NV), and lane-vector j of lane l is the slot
+// 64 * j + l of that run. Every load is issued before any selection work, then
+//   pass 1  as the loads land, two signed-integer maxima per lane over the
+//           lane-vectors with no penalty state and no masked element; every
+//           report is a real element, so the k-th largest report key is a
+//           lower bound of the slice's k-th largest configured key;
+//   select  that k-th largest report (LDS radix select) -> thr;
+//   pass 2  lane-vectors whose raw maximum reaches thr are staged in LDS;
+//   exact   one lane per staged lane-vector computes configured keys and
+//           appends keys >= thr to the candidate list.
+// Penalties that never raise a logit (repetition >= 1, frequency and presence
+// >= 0) keep configured <= raw, so the raw test is conservative for penalised
+// tokens too. Other settings take penalised tokens out of the vector passes
+// and evaluate each one from the history table instead (one gather per id).
+template <typename Elem, int EPV, int NV, int PEN>
 __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     constexpr int HPT = (kMaxHistory + kBlock - 1) / kBlock;  // history ids per lane
-    constexpr uint32_t CHV = (uint32_t)kBlock * VPL;           // lane-vectors per stage
+    constexpr int BW = (int)((slice_bitmap_words((uint32_t)kBlock * NV * EPV, EPV) + kBlock - 1u) / kBlock);
+    constexpr int LW = (NV + 31) / 32;
+    constexpr uint32_t kFull = EPV == 32 ? 0xffffffffu : ((1u << EPV) - 1u);
     constexpr bool history = PEN == 2;
     using VT = VecTraits<Elem, EPV>;
     using vec_t = typename VT::load_t;
+    constexpr uint32_t kVecBytes = (uint32_t)sizeof(vec_t);
     __shared__ SharedSmall sm;
     extern __shared__ __align__(16) uint32_t s_dyn[];
-    uint32_t *s_hash = s_dyn;                             // [hash_slots]
-    uint32_t *s_bitmap = s_hash + a.hash_slots;           // [bitmap_words]
-    uint2 *s_cand = (uint2 *)(s_bitmap + a.bitmap_words);  // [kStreamCandCap], later merge / top-p scratch
-    uint2 *s_sorted = s_cand + kStreamCandCap;            // [kcap]
+    vec_t *s_svec = (vec_t *)s_dyn;                                // [kStageCap]
+    uint32_t *s_sslot = (uint32_t *)(s_svec + kStageCap);          // [kStageCap]
+    uint2 *s_cand = (uint2 *)(s_sslot + kStageCap);                // [kStreamCandCap], later finish scratch
+    uint2 *s_sorted = s_cand + kStreamCandCap;                     // [kcap]
+    uint32_t *s_hash = (uint32_t *)(s_sorted + a.kcap);            // [hash_slots]
+    uint32_t *s_pen = s_hash + a.hash_slots;                       // [bitmap_words] when PEN != 0
+    uint32_t *s_allow = s_pen + (PEN != 0 ? a.bitmap_words : 0u);  // [bitmap_words] with a mask
     uint2 *s_big = s_cand;
 
     const uint32_t tid = threadIdx.x;
-    const uint32_t lane = lane_id();
-    const uint32_t wave = tid >> 6;
     const uint32_t logical = xcd_remap(blockIdx.x, gridDim.x);
     const uint32_t row = logical / a.slices;
     const uint32_t slice = logical % a.slices;
@@ -713,41 +781,32 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     k = k < 1u ? 1u : (k > a.kcap ? a.kcap : k);
     const uint32_t valid_min = sampled ? kMinFiniteKey : kNegInfKey;
     const uint32_t masked_key = sampled ? 0u : kNegInfKey;
+    const bool mask = a.allowed != nullptr;
+    const bool lowering = P.repetition_penalty >= 1.0f && P.frequency_penalty >= 0.0f && P.presence_penalty >= 0.0f;
 
-    // The slice owns full EPV-element lane-vectors [v0, v1); the last slice
-    // also owns the V % EPV tail elements, one per lane.
     const uint32_t nfull = a.nvec;
     const uint32_t v0 = min(slice * a.vec_per_slice, nfull);
     const uint32_t v1 = min(v0 + a.vec_per_slice, nfull);
-    const uint32_t nchunks = (v1 - v0 + CHV - 1u) / CHV;
     const bool last_slice = slice == a.slices - 1u;
     const uint32_t tok0 = v0 * EPV;
     const uint32_t tok1 = last_slice ? a.vocab : v1 * EPV;
+    const uint32_t bm_base = tok0 & ~31u;
+    const uint32_t bm_n = tok1 > tok0 ? ((tok1 - 1u) >> 5) - (bm_base >> 5) + 1u : 0u;
     const uint32_t tail_id = nfull * EPV + tid;
     const bool has_tail = last_slice && tail_id < a.vocab;
 
     const Elem *lrow = (const Elem *)a.logits + (uint64_t)row * a.ld;
-    const uint32_t *arow = MASK ? a.allowed + (uint64_t)row * a.allowed_stride : nullptr;
+    const uint32_t *arow = mask ? a.allowed + (uint64_t)row * a.allowed_stride : nullptr;
     const uint32_t *srow = PEN == 1 ? a.seen + (uint64_t)row * a.seen_stride : nullptr;
-    const uint32_t last_slot = nfull - 1u;
-
-    // Register ring of kStages stages; a stage is VPL lane-vectors per lane
-    // plus their mask / seen words. Addresses are clamped into the row, so the
-    // loads never branch and all stages of a lane stay in flight together.
-    vec_t ring[kStages][VPL];
-    uint32_t mring[kStages][VPL], sring[kStages][VPL];
-    auto issue = [&](uint32_t c, vec_t (&rv)[VPL], uint32_t (&mv)[VPL], uint32_t (&sv)[VPL]) {
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            const uint32_t ls = min(v0 + c * CHV + (uint32_t)i * kBlock + tid, last_slot);
-            rv[i] = *(const vec_t *)(lrow + (uint64_t)ls * EPV);
-            if constexpr (MASK) mv[i] = arow[(ls * EPV) >> 5];
-            if constexpr (PEN == 1) sv[i] = srow[(ls * EPV) >> 5];
-        }
-    };
 
     PHASE_MARK(0);
-    // 1. history ids, then the first kStages stages
+    // 1. loads: history ids and bitmap words first (they are needed first),
+    // then the first half of the slice's lane-vectors through a buffer
+    // resource bounded by v1 (a slot past the slice reads as zero and is never
+    // used). A wave owns 64 * NV consecutive slots, so the loads of a lane sit
+    // 64 slots apart and share one offset register per 4 KiB.
+    const uint32_t lane = lane_id();
+    const uint32_t wbase = (tid >> 6) * 64u * (uint32_t)NV + lane;  // slot of lane-vector 0, relative to v0
     uint32_t hist[history ? HPT : 1];
     uint32_t hlen = 0;
     if constexpr (history) {
@@ -757,313 +816,315 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         for (int h = 0; h < HPT; ++h) hist[h] = hrow[min(tid + (uint32_t)h * kBlock, hlast)];
         hlen = min(a.history_len[row], a.history_stride);
     }
-    const uint32_t tail_at = min(tail_id, a.vocab - 1u);
-    const uint32_t tail_bits = f2u(load_elem<Elem>(lrow, tail_at));
-    uint32_t tail_m = 0xffffffffu, tail_s = 0u;
-    if constexpr (MASK) tail_m = arow[tail_at >> 5];
-    if constexpr (PEN == 1) tail_s = srow[tail_at >> 5];
-    issue(0u, ring[0], mring[0], sring[0]);
-    issue(1u, ring[1], mring[1], sring[1]);
-    issue(2u, ring[2], mring[2], sring[2]);
-    issue(3u, ring[3], mring[3], sring[3]);
+    const uint32_t bm_last = bm_n ? bm_n - 1u : 0u;
+    uint32_t mw[BW];
+    if (mask) {
+#pragma unroll
+        for (int i = 0; i < BW; ++i) mw[i] = arow[(bm_base >> 5) + min(tid + (uint32_t)i * kBlock, bm_last)];
+    }
+    uint32_t sw[PEN == 1 ? BW : 1];
+    if constexpr (PEN == 1) {
+#pragma unroll
+        for (int i = 0; i < BW; ++i) sw[i] = srow[(bm_base >> 5) + min(tid + (uint32_t)i * kBlock, bm_last)];
+    }
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(lrow + (uint64_t)v0 * EPV), (short)0, (int)((v1 - v0) * kVecBytes), 0x00020000);
+    vec_t data[NV];
+    auto load = [&](int j) __attribute__((always_inline)) {
+        const uint32_t off = (wbase + (uint32_t)j * 64u) * kVecBytes;
+        if constexpr (kVecBytes == 16) data[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
+        else if constexpr (kVecBytes == 4) data[j] = u2f(__builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, 0));
+        else data[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
+    };
+    constexpr int NA = NV / 2;  // issued before the LDS set-up, the rest after it
+#pragma unroll
+    for (int j = 0; j < NA; ++j) load(j);
 
-    // 2. LDS state: counters, and the slice's history ids -> bitmap + hash
+    // 2. LDS state: counters, mask / seen words of the slice (bits outside
+    // [tok0, tok1) cleared), history ids -> bitmap + id -> count table
     if constexpr (history) {
         for (uint32_t i = tid; i < a.hash_slots; i += kBlock) s_hash[i] = kHashEmpty;
-        for (uint32_t i = tid; i < a.bitmap_words; i += kBlock) s_bitmap[i] = 0u;
+        for (uint32_t i = tid; i < bm_n; i += kBlock) s_pen[i] = 0u;
     }
-    if (tid == 0) sm.flag[1] = 0u;  // candidates appended
+    if (tid == 0) {
+        sm.flag[1] = 0u;  // candidates
+        sm.flag[2] = 0u;  // staged lane-vectors
+        sm.ones[0] = 0xffffffffu;
+    }
+    auto range_bits = [&](uint32_t w) __attribute__((always_inline)) -> uint32_t {
+        const uint32_t t = bm_base + w * 32u;
+        uint32_t m = 0xffffffffu;
+        if (t < tok0) m &= 0xffffffffu << (tok0 - t);
+        if (t + 32u > tok1) m &= (tok1 - t) >= 32u ? 0xffffffffu : ((1u << (tok1 - t)) - 1u);
+        return m;
+    };
+    uint32_t any_allowed = mask ? 0u : (tok1 > tok0 ? 1u : 0u);
+    if (mask) {
+#pragma unroll
+        for (int i = 0; i < BW; ++i) {
+            const uint32_t w = tid + (uint32_t)i * kBlock;
+            if (w < bm_n) {
+                const uint32_t v = mw[i] & range_bits(w);
+                s_allow[w] = v;
+                any_allowed |= v ? 1u : 0u;
+            }
+        }
+    }
+    if constexpr (PEN == 1) {
+#pragma unroll
+        for (int i = 0; i < BW; ++i) {
+            const uint32_t w = tid + (uint32_t)i * kBlock;
+            if (w < bm_n) s_pen[w] = sw[i] & range_bits(w);
+        }
+    }
     lds_sync();
     if constexpr (history) {
 #pragma unroll
         for (int h = 0; h < HPT; ++h) {
             const uint32_t id = hist[h];
             if (tid + (uint32_t)h * kBlock < hlen && id >= tok0 && id < tok1) {
-                const uint32_t o = id - tok0;
-                atomicOr(&s_bitmap[o >> 5], 1u << (o & 31u));
+                const uint32_t o = id - bm_base;
+                atomicOr(&s_pen[o >> 5], 1u << (o & 31u));
                 hash_insert(s_hash, a.log2_slots, id);
             }
         }
-        lds_sync();
     }
+#pragma unroll
+    for (int j = NA; j < NV; ++j) load(j);
+    if constexpr (history) lds_sync();
     PHASE_MARK(1);
 
-    // 3. stream the stages
-    uint32_t tmax = 0, best_id = kPadId;  // greedy: lane best; sampled: lane max so far
-    uint32_t any_allowed = 0, has_nan = 0;
-    uint32_t thr = 1u;                    // sampled: keys >= thr are kept (block-uniform)
-    auto take = [&](uint32_t key, uint32_t id) __attribute__((always_inline)) {
-        if (key > tmax || (key == tmax && key != 0u && id < best_id)) {
-            tmax = key;
-            best_id = id;
+    // 3. pass 1: lane reports from lane-vectors whose every element is valid,
+    // allowed and free of penalty state
+    const uint32_t nval = v1 - v0 > wbase ? (v1 - v0 - wbase + 63u) / 64u : 0u;  // valid lane-vectors of this lane
+    const uint32_t *mask_words = mask ? s_allow : sm.ones;
+    // 1a: per lane-vector flags as bit masks (ok = every element valid,
+    // allowed and free of penalty state; live = some element valid and allowed)
+    uint32_t okm[LW], live[LW];
+#pragma unroll
+    for (int i = 0; i < LW; ++i) {
+        okm[i] = 0u;
+        live[i] = 0u;
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const bool valid = (uint32_t)j < nval;
+        uint32_t okb = valid ? kFull : 0u, anyb = okb;
+        {
+            // branch-free: a row without a mask reads an all-ones word
+            const uint32_t off = valid ? (v0 + wbase + (uint32_t)j * 64u) * EPV - bm_base : 0u;
+            const uint32_t ab = (mask_words[mask ? off >> 5 : 0u] >> (mask ? off & 31u : 0u)) & kFull;
+            okb &= ab;
+            anyb &= ab;
+            if constexpr (PEN != 0) okb = ((s_pen[off >> 5] >> (off & 31u)) & kFull) ? 0u : okb;
+        }
+        okm[j >> 5] |= (okb == kFull ? 1u : 0u) << (j & 31);
+        live[j >> 5] |= (anyb ? 1u : 0u) << (j & 31);
+        // bound how far the bitmap reads are hoisted: each holds a VGPR
+        // while the whole slice is already resident
+        if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+    }
+    // 1b: the two report accumulators, in load order
+    uint32_t acc0 = VT::kAccInit, acc1 = VT::kAccInit;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t vm = VT::vmax(data[j]);
+        const bool ok = (okm[j >> 5] >> (j & 31)) & 1u;
+        if (j & 1) acc1 = ok ? VT::merge(acc1, vm) : acc1;
+        else acc0 = ok ? VT::merge(acc0, vm) : acc0;
+    }
+
+    // 4. thr = the k-th largest report key (1 when fewer than k reports)
+    constexpr int NR = 2 * VT::kReports;
+    uint32_t rep[NR];
+#pragma unroll
+    for (int r = 0; r < VT::kReports; ++r) {
+        const uint32_t b0 = VT::report_bits(acc0, r), b1 = VT::report_bits(acc1, r);
+        uint32_t k0 = b0 == 0x80000000u ? 0u : raw_order_key(b0);
+        uint32_t k1 = b1 == 0x80000000u ? 0u : raw_order_key(b1);
+        rep[2 * r] = k0 < valid_min ? 0u : k0;
+        rep[2 * r + 1] = k1 < valid_min ? 0u : k1;
+    }
+    uint32_t unused_count;
+    uint32_t thr = radix_threshold<NR>(rep, k, sizeof(Elem) == 2 ? 2 : 3, sm.hist, sm.sel, unused_count);
+    thr = thr < 1u ? 1u : thr;
+    PHASE_MARK(2);
+
+    // Pass 2 recomputes the lane-vector maxima: keeping the pass-1 values
+    // alive would cost NV more VGPRs than the slice can spare.
+#pragma unroll
+    for (int j = 0; j < NV; ++j) asm volatile("" : "+v"(data[j]));
+
+    // 5. pass 2: stage the lane-vectors that can hold a key >= thr. Masked
+    // lane-vectors are skipped unless a masked token could still qualify
+    // (greedy rows treat masked tokens as -inf).
+    const bool skip_dead = sampled || thr > kNegInfKey;
+    auto stage = [&](int j, bool go) __attribute__((always_inline)) {
+        if (go) {
+            const uint32_t pos = atomicAdd(&sm.flag[2], 1u);
+            if (pos < kStageCap) {
+                s_svec[pos] = data[j];
+                s_sslot[pos] = v0 + wbase + (uint32_t)j * 64u;
+            }
         }
     };
+    if (thr > kZeroKey) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const bool lv = skip_dead ? ((live[j >> 5] >> (j & 31)) & 1u) : ((uint32_t)j < nval);
+            stage(j, lv && VT::ge_pos(VT::vmax(data[j]), thr));
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const bool lv = skip_dead ? ((live[j >> 5] >> (j & 31)) & 1u) : ((uint32_t)j < nval);
+            stage(j, lv && VT::upper(data[j]) >= thr);
+        }
+    }
+    // the V % EPV tail of the last slice, one element per lane (loaded late:
+    // it is rare and holding it across the passes costs a VGPR)
+    const uint32_t tail_bits = has_tail ? f2u(load_elem<Elem>(lrow, tail_id)) : 0u;
+    // greedy rows: any NaN selects the reference's lane-structure replay
+    uint32_t has_nan = 0u;
+    if (!sampled) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) has_nan |= ((uint32_t)j < nval && VT::has_nan(data[j])) ? 1u : 0u;
+        if (has_tail) has_nan |= ((tail_bits & 0x7fffffffu) > 0x7f800000u) ? 1u : 0u;
+        const float pq = P.repetition_penalty + P.frequency_penalty + P.presence_penalty;
+        if (PEN != 0 && !(pq - pq == 0.0f)) has_nan = 1u;  // non-finite penalty parameters
+    }
+    PHASE_MARK(3);
+
+    // 6. exact keys of the staged lane-vectors, the tail, and (for penalties
+    // that may raise a logit) every penalised token from the history state
     auto push = [&](uint32_t key, uint32_t id) __attribute__((always_inline)) {
         const uint32_t pos = atomicAdd(&sm.flag[1], 1u);
         if (pos < kStreamCandCap) s_cand[pos] = make_uint2(key, id);
     };
-    // A token with penalty state competes with its configured value.
-    auto patch = [&](uint32_t bits, uint32_t id, uint32_t count) __attribute__((always_inline)) {
+    auto pen_key = [&](uint32_t bits, bool allowed, uint32_t count) __attribute__((always_inline)) -> uint32_t {
+        if (!allowed) return masked_key;
         const float v = configured_logit(u2f(bits), true, count, P.repetition_penalty, P.frequency_penalty,
                                          P.presence_penalty);
-        uint32_t key = order_key(v);
-        has_nan |= (v != v) ? 1u : 0u;
-        key = key < valid_min ? 0u : key;
-        if (!sampled) take(key, id);
-        else if (key >= thr && key != 0u) push(key, id);
+        const uint32_t key = order_key(v);
+        return key < valid_min ? 0u : key;
     };
-    // Penalties that never raise a logit (repetition >= 1, frequency and
-    // presence >= 0) cannot lift a token above a bound that its raw value does
-    // not reach, so tokens with penalty state need work only where their raw
-    // value passes; other settings patch every such token.
-    const bool lowering = P.repetition_penalty >= 1.0f && P.frequency_penalty >= 0.0f && P.presence_penalty >= 0.0f;
-
-    // Exact per-element work on one lane-vector. mode 0: per-lane maximum and
-    // flags (first pass over a sampled row's first stage); 1 and 2: append
-    // keys >= thr; 3: greedy per-lane best. In modes 1-3 an element whose raw
-    // key cannot pass is skipped before its configured value is computed.
-    auto exact_vec = [&](const vec_t &vec, uint32_t id0, uint32_t valid, uint32_t abits, uint32_t pbits, int mode) __attribute__((always_inline)) {
-#pragma unroll
-        for (int e = 0; e < EPV; ++e) {
-            const uint32_t bits = VT::bits(vec, e);
-            const bool in = (valid >> e) & 1u, allowed = (abits >> e) & 1u, pen = (pbits >> e) & 1u;
-            if (mode == 0) any_allowed |= (in && allowed) ? 1u : 0u;
-            if (!in) continue;
-            if (mode != 0) {
-                const uint32_t raw_up = f32_key_upper(bits);
-                const bool can = mode == 3 ? (raw_up > tmax || tmax == 0u) : raw_up >= thr;
-                if (!can || (pen && !lowering)) continue;  // a raised value is patched separately
-            }
-            uint32_t key;
-            if (!allowed) {
-                key = masked_key;
-            } else if (pen) {
-                const uint32_t id = id0 + (uint32_t)e;
-                const uint32_t count = history ? hash_lookup(s_hash, a.log2_slots, id) : 1u;
-                const float v = configured_logit(u2f(bits), true, count, P.repetition_penalty, P.frequency_penalty,
-                                                 P.presence_penalty);
-                has_nan |= (v != v) ? 1u : 0u;
-                key = order_key(v);
-            } else {
-                has_nan |= ((bits & 0x7fffffffu) > 0x7f800000u) ? 1u : 0u;
-                key = raw_order_key(bits);
-            }
+    auto exact_elem = [&](uint32_t bits, uint32_t id) __attribute__((always_inline)) {
+        const uint32_t off = id - bm_base;
+        const bool allowed = !mask || ((s_allow[off >> 5] >> (off & 31u)) & 1u);
+        bool pen = false;
+        if constexpr (PEN != 0) pen = (s_pen[off >> 5] >> (off & 31u)) & 1u;
+        uint32_t key;
+        if (pen) {
+            if (!lowering) return;  // evaluated from the history state below
+            key = pen_key(bits, allowed, history ? hash_lookup(s_hash, a.log2_slots, id) : 1u);
+        } else {
+            key = allowed ? raw_order_key(bits) : masked_key;
             key = key < valid_min ? 0u : key;
-            if (mode == 0 || mode == 3) {
-                take(key, id0 + (uint32_t)e);
-            } else if (key >= thr && key != 0u) {
-                push(key, id0 + (uint32_t)e);
-            }
         }
+        if (key >= thr && key != 0u) push(key, id);
     };
-    // Modes as above; modes 2 (later stages of sampled rows) and 3 (greedy)
-    // first take a packed-integer upper bound of the lane-vector's raw keys and
-    // run the exact code only where it can matter.
-    auto process = [&](uint32_t c, const vec_t (&rv)[VPL], const uint32_t (&mv)[VPL], const uint32_t (&sv)[VPL],
-                       int mode) {
-#ifdef NERVE_DEBUG_NOPROCESS
-        // profiling builds only: consume the ring without any selection work
+    if (has_tail) exact_elem(tail_bits, tail_id);
+    lds_sync();
+    const uint32_t nstaged = sm.flag[2];
+    if (nstaged <= kStageCap) {
+        for (uint32_t i = tid; i < nstaged; i += kBlock) {
+            const vec_t vec = s_svec[i];
+            const uint32_t id0 = s_sslot[i] * EPV;
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) tmax = max(tmax, VT::bits(rv[i], 0));
-        return;
-#endif
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) {
-            const uint32_t vi = (uint32_t)i * kBlock + tid;
-            const uint32_t slot = v0 + c * CHV + vi;
-            const uint32_t id0 = slot * EPV;
-            const vec_t vec = rv[i];
-            const uint32_t valid = slot < v1 ? ((1u << EPV) - 1u) : 0u;
-            uint32_t pbits = 0u;
-            if constexpr (history) pbits = valid ? s_bitmap[(id0 - tok0) >> 5] >> ((id0 - tok0) & 31u) : 0u;
-            if constexpr (PEN == 1) pbits = sv[i] >> (id0 & 31u);
-            uint32_t abits = 0xffffffffu;
-            if constexpr (MASK) abits = mv[i] >> (id0 & 31u);
-            pbits &= valid & abits;
-            if (mode <= 1) {
-                exact_vec(vec, id0, valid, abits, pbits, mode);
-            } else {
-                const uint32_t live = valid & abits;
-                any_allowed |= live ? 1u : 0u;
-                if (mode == 3) has_nan |= (valid && VT::has_nan(vec)) ? 1u : 0u;
-                bool go = false;
-                if (live) {
-                    const uint32_t up = VT::upper(vec);
-                    go = mode == 2 ? up >= thr : (up > tmax || tmax == 0u);
+            for (int e = 0; e < EPV; ++e) exact_elem(VT::bits(vec, e), id0 + (uint32_t)e);
+        }
+        if (PEN != 0 && !lowering) {
+            auto pen_token = [&](uint32_t id, uint32_t count) __attribute__((always_inline)) {
+                const uint32_t off = id - bm_base;
+                const bool allowed = !mask || ((s_allow[off >> 5] >> (off & 31u)) & 1u);
+                const uint32_t key = pen_key(f2u(load_elem<Elem>(lrow, id)), allowed, count);
+                if (key >= thr && key != 0u) push(key, id);
+            };
+            if constexpr (history) {
+                for (uint32_t i = tid; i < a.hash_slots; i += kBlock) {
+                    const uint32_t cur = s_hash[i];
+                    if (cur != kHashEmpty) pen_token(cur >> 12, cur & 0xfffu);
                 }
-                if (go) exact_vec(vec, id0, valid, abits, pbits, mode);
-#ifdef NERVE_PHASE_TIMING
-                {
-                    const uint64_t bw = __ballot(go);
-                    if (lane == 0u) {
-                        DBG_ADD(0, (uint32_t)__popcll(bw));
-                        DBG_ADD(1, bw ? 1u : 0u);
+            } else if constexpr (PEN == 1) {
+                for (uint32_t w = tid; w < bm_n; w += kBlock) {
+                    uint32_t bits = s_pen[w];
+                    while (bits) {
+                        const uint32_t b = (uint32_t)__builtin_ctz(bits);
+                        bits &= bits - 1u;
+                        pen_token(bm_base + w * 32u + b, 1u);
                     }
                 }
-#endif
             }
-            if (mode != 0 && !lowering) {
-                while (pbits) {
-                    const uint32_t e = (uint32_t)__builtin_ctz(pbits);
-                    pbits &= pbits - 1u;
-                    const uint32_t id = id0 + e;
-                    patch(VT::bits_dyn(vec, e), id, history ? hash_lookup(s_hash, a.log2_slots, id) : 1u);
-                }
-            }
-        }
-    };
-    // thr after the first stage: first 16 bits of the k-th largest per-lane
-    // maximum (at least k keys are >= it). Later refreshes: the exact k-th
-    // largest key among the candidates kept so far (every key >= the old thr
-    // is among them, so it is the running k-th largest). thr only rises.
-    auto first_threshold = [&]() __attribute__((always_inline)) {
-        uint32_t unused;
-        const uint32_t tm[1] = {tmax};
-        const uint32_t t = radix_threshold<1>(tm, k, 2, sm.hist, sm.sel, unused);
-        thr = t > thr ? t : thr;
-    };
-    auto refresh_threshold = [&]() __attribute__((always_inline)) {
-        lds_sync();
-        const uint32_t C = sm.flag[1];
-        if (C >= k && C <= kStreamCandCap) {
-            auto cand_key = [&](uint32_t i) __attribute__((always_inline)) -> uint32_t { return s_cand[i].x; };
-            uint32_t unused;
-            const uint32_t t = radix_threshold_fn(0u, C, k, sm.hist, sm.sel, unused, cand_key);
-            thr = t > thr ? t : thr;
-        }
-    };
-
-    // One ring slot per call, addressed at compile time: the processing of
-    // stage c overlaps the loads of stages c+1 .. c+3, and the refill of the
-    // slot is issued unconditionally (addresses past the slice clamp to the
-    // last slot and are masked out), so every path has the same loads in
-    // flight and the compiler waits only for the slot about to be used.
-    auto stage = [&](uint32_t c, vec_t (&rv)[VPL], uint32_t (&mv)[VPL], uint32_t (&sv)[VPL], bool may_be_first) {
-        if (c < nchunks) {
-            if (!sampled) {
-                process(c, rv, mv, sv, 3);
-            } else if (may_be_first && c == 0u) {
-                process(0u, rv, mv, sv, 0);
-                first_threshold();
-                process(0u, rv, mv, sv, 1);
-            } else {
-                process(c, rv, mv, sv, 2);
-                if (c == 1u || c == 3u || c == 7u || c == 15u) refresh_threshold();
-            }
-        }
-        issue(c + kStages, rv, mv, sv);
-    };
-    for (uint32_t c0 = 0; c0 < nchunks; c0 += kStages) {
-        stage(c0 + 0u, ring[0], mring[0], sring[0], true);
-        stage(c0 + 1u, ring[1], mring[1], sring[1], false);
-        stage(c0 + 2u, ring[2], mring[2], sring[2], false);
-        stage(c0 + 3u, ring[3], mring[3], sring[3], false);
-    }
-    PHASE_MARK(2);
-
-    // the tail elements of the last slice
-    if (has_tail) {
-        bool allowed = true;
-        if constexpr (MASK) allowed = (tail_m >> (tail_at & 31u)) & 1u;
-        uint32_t pbit = 0u;
-        if constexpr (history) {
-            const uint32_t o = tail_id - tok0;
-            pbit = (s_bitmap[o >> 5] >> (o & 31u)) & 1u;
-        }
-        if constexpr (PEN == 1) pbit = (tail_s >> (tail_at & 31u)) & 1u;
-        any_allowed |= allowed ? 1u : 0u;
-        has_nan |= (allowed && (tail_bits & 0x7fffffffu) > 0x7f800000u) ? 1u : 0u;
-        if (pbit && allowed) {
-            patch(tail_bits, tail_id, history ? hash_lookup(s_hash, a.log2_slots, tail_id) : 1u);
-        } else {
-            uint32_t key = allowed ? raw_order_key(tail_bits) : masked_key;
-            key = key < valid_min ? 0u : key;
-            take(key, tail_id);
-            if (sampled && key >= thr && key != 0u) push(key, tail_id);
         }
     }
+    lds_sync();
 
     RowCtx ctx;
     ctx.logits_row = lrow;
     ctx.allowed_row = arow;
     ctx.seen_row = srow;
     ctx.hash = s_hash;
-    ctx.bitmap = s_bitmap;
+    ctx.bitmap = s_pen;
     ctx.log2_slots = a.log2_slots;
-    ctx.tok0 = tok0;
+    ctx.tok0 = bm_base;
     ctx.rep = P.repetition_penalty;
     ctx.freq = P.frequency_penalty;
     ctx.pres = P.presence_penalty;
     ctx.history = history;
 
-    // slice flags: bit 0 = some token allowed, bit 1 = some configured value is NaN
+    // slice flags: bit 0 = some token allowed, bit 1 = greedy row holds a NaN
     const uint32_t fsum = block_sum(any_allowed | (has_nan << 16), sm.scan);
     const uint32_t flags_slice = ((fsum & 0xffffu) ? 1u : 0u) | ((fsum >> 16) ? 2u : 0u);
-    PHASE_MARK(3);
+    PHASE_MARK(4);
 
-    // 4. selection -> s_sorted[0 .. n_out)
-    uint32_t n_out = 0;
-    if (!sampled) {
-        const uint64_t packed = tmax ? (((uint64_t)tmax << 32) | (uint64_t)(~best_id)) : 0ull;
-        const uint64_t m = block_max_u64(packed, sm.red);
-        if (m != 0ull) {
-            if (tid == 0) s_sorted[0] = make_uint2((uint32_t)(m >> 32), ~(uint32_t)m);
-            n_out = 1;
+    // 7. selection -> s_sorted[0 .. n_out)
+    uint32_t C = sm.flag[1];
+    if (nstaged > kStageCap || C > kStreamCandCap) {
+        // Skewed slice (for example a constant row): exact selection recomputed
+        // from memory. The k-th largest key kv, then the `need` smallest ids
+        // among keys == kv.
+        auto key_at = [&](uint32_t tt) __attribute__((always_inline)) -> uint32_t {
+            const uint32_t key = order_key(configured_at<Elem>(ctx, tt));
+            return key < valid_min ? 0u : key;
+        };
+        uint32_t count_ge;
+        const uint32_t kv = radix_threshold_fn(tok0, tok1, k, sm.hist, sm.sel, count_ge, key_at);
+        uint32_t gt = 0;
+        for (uint32_t tt = tok0 + tid; tt < tok1; tt += kBlock) gt += key_at(tt) > kv ? 1u : 0u;
+        const uint32_t G = block_sum(gt, sm.scan);
+        const uint32_t need = k > G ? k - G : 0u;
+        auto tie_at = [&](uint32_t tt) __attribute__((always_inline)) -> uint32_t { return key_at(tt) == kv ? ~tt : 0u; };
+        uint32_t ties_ge;
+        const uint32_t id_cut = need ? ~radix_threshold_fn(tok0, tok1, need, sm.hist, sm.sel, ties_ge, tie_at) : 0u;
+        if (tid == 0) sm.flag[1] = 0u;
+        lds_sync();
+        for (uint32_t tt = tok0 + tid; tt < tok1; tt += kBlock) {
+            const uint32_t key = key_at(tt);
+            if (key != 0u && (key > kv || (key == kv && need && tt <= id_cut))) {
+                const uint32_t q = atomicAdd(&sm.flag[1], 1u);
+                if (q < kStreamCandCap) s_cand[q] = make_uint2(key, tt);
+            }
         }
         lds_sync();
-    } else {
-        uint32_t C = sm.flag[1];
-        PHASE_MARK(4);
-        if (tid == 0) {
-            DBG_SET(2, C);
-            DBG_SET(3, thr);
-        }
-        if (C > kStreamCandCap) {
-            // Skewed slice: exact selection recomputed from memory (rare). The
-            // k-th largest key kv, then the `need` smallest ids among keys == kv.
-            auto key_at = [&](uint32_t tt) __attribute__((always_inline)) -> uint32_t {
-                const uint32_t key = order_key(configured_at<Elem>(ctx, tt));
-                return key < valid_min ? 0u : key;
-            };
-            uint32_t count_ge;
-            const uint32_t kv = radix_threshold_fn(tok0, tok1, k, sm.hist, sm.sel, count_ge, key_at);
-            uint32_t gt = 0;
-            for (uint32_t tt = tok0 + tid; tt < tok1; tt += kBlock) gt += key_at(tt) > kv ? 1u : 0u;
-            const uint32_t G = block_sum(gt, sm.scan);
-            const uint32_t need = k - G;
-            auto tie_at = [&](uint32_t tt) __attribute__((always_inline)) -> uint32_t { return key_at(tt) == kv ? ~tt : 0u; };
-            uint32_t ties_ge;
-            const uint32_t id_cut = ~radix_threshold_fn(tok0, tok1, need, sm.hist, sm.sel, ties_ge, tie_at);
-            if (tid == 0) sm.flag[1] = 0u;
-            lds_sync();
-            for (uint32_t tt = tok0 + tid; tt < tok1; tt += kBlock) {
-                const uint32_t key = key_at(tt);
-                if (key > kv || (key == kv && tt <= id_cut)) {
-                    const uint32_t q = atomicAdd(&sm.flag[1], 1u);
-                    if (q < kStreamCandCap) s_cand[q] = make_uint2(key, tt);
-                }
-            }
-            lds_sync();
-            C = min(sm.flag[1], kStreamCandCap);
-        }
-        // rank sort (ids are distinct, so ranks are a permutation)
-        for (uint32_t i = tid; i < C; i += kBlock) {
-            const uint2 e = s_cand[i];
-            uint32_t r0 = 0, r1 = 0, r2 = 0, r3 = 0;
-            uint32_t j = 0;
-            for (; j + 4u <= C; j += 4u) {
-                r0 += entry_better(s_cand[j], e) ? 1u : 0u;
-                r1 += entry_better(s_cand[j + 1u], e) ? 1u : 0u;
-                r2 += entry_better(s_cand[j + 2u], e) ? 1u : 0u;
-                r3 += entry_better(s_cand[j + 3u], e) ? 1u : 0u;
-            }
-            for (; j < C; ++j) r0 += entry_better(s_cand[j], e) ? 1u : 0u;
-            const uint32_t r = r0 + r1 + r2 + r3;
-            if (r < k) s_sorted[r] = e;
-        }
-        n_out = C < k ? C : k;
-        lds_sync();
+        C = min(sm.flag[1], kStreamCandCap);
     }
+    // rank sort (ids are distinct, so ranks are a permutation)
+    for (uint32_t i = tid; i < C; i += kBlock) {
+        const uint2 e = s_cand[i];
+        uint32_t r0 = 0, r1 = 0, r2 = 0, r3 = 0;
+        uint32_t j = 0;
+        for (; j + 4u <= C; j += 4u) {
+            r0 += entry_better(s_cand[j], e) ? 1u : 0u;
+            r1 += entry_better(s_cand[j + 1u], e) ? 1u : 0u;
+            r2 += entry_better(s_cand[j + 2u], e) ? 1u : 0u;
+            r3 += entry_better(s_cand[j + 3u], e) ? 1u : 0u;
+        }
+        for (; j < C; ++j) r0 += entry_better(s_cand[j], e) ? 1u : 0u;
+        const uint32_t r = r0 + r1 + r2 + r3;
+        if (r < k) s_sorted[r] = e;
+    }
+    const uint32_t n_out = C < k ? C : k;
+    lds_sync();
     PHASE_MARK(5);
 
     // the sign of a zero survivor comes from its own configured value
@@ -1077,7 +1138,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     __syncthreads();
     PHASE_MARK(6);
 
-    // 5. publish: with several slices the sorted list goes to scratch and the
+    // 8. publish: with several slices the sorted list goes to scratch and the
     // finish kernel merges the row; a single slice finishes here.
     if (a.slices > 1) {
         uint2 *lists = a.scratch_lists + (uint64_t)(row * a.slices + slice) * a.kcap;
@@ -1173,11 +1234,15 @@ __global__ void record_tokens_kernel(uint32_t *seen, uint32_t seen_stride, uint3
 
 // ---- launch ------------------------------------------------------------------
 
-template <typename Elem, int EPV, int VPL, bool MASK, int PEN>
+template <typename Elem, int EPV>
+static constexpr uint32_t stage_bytes() {
+    return kStageCap * ((uint32_t)sizeof(typename VecTraits<Elem, EPV>::load_t) + 4u);
+}
+
+template <typename Elem, int EPV, int NV, int PEN>
 static hipError_t launch_one(const StepArgs &a0, hipStream_t stream) {
     StepArgs a = a0;
-    a.dyn_lds_bytes = a.hash_slots * 4u + a.bitmap_words * 4u + kStreamCandCap * 8u + a.kcap * 8u;
-    auto kern = sample_rows_kernel<Elem, EPV, VPL, MASK, PEN>;
+    auto kern = sample_rows_kernel<Elem, EPV, NV, PEN>;
     hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)a.dyn_lds_bytes);
     if (e != hipSuccess) return e;
@@ -1194,18 +1259,68 @@ static hipError_t launch_one(const StepArgs &a0, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <typename Elem, int EPV, int VPL>
-static hipError_t launch_variant(const StepArgs &a, hipStream_t stream) {
-    const bool mask = a.allowed != nullptr;
-    const int pen = a.history ? 2 : (a.seen ? 1 : 0);
-    if (mask) {
-        if (pen == 2) return launch_one<Elem, EPV, VPL, true, 2>(a, stream);
-        if (pen == 1) return launch_one<Elem, EPV, VPL, true, 1>(a, stream);
-        return launch_one<Elem, EPV, VPL, true, 0>(a, stream);
+template <typename Elem, int EPV, int NV>
+static hipError_t launch_pen(const StepArgs &a, hipStream_t stream) {
+    if (a.history) return launch_one<Elem, EPV, NV, 2>(a, stream);
+    if (a.seen) return launch_one<Elem, EPV, NV, 1>(a, stream);
+    return launch_one<Elem, EPV, NV, 0>(a, stream);
+}
+
+// Lane-vectors per lane (NV) of the compiled slice kernels, per variant: the
+// largest keep the whole kernel within 256 VGPRs without spills.
+static const uint32_t kBf16NV[] = {8, 16, 24, 32, 40};
+static const uint32_t kF32NV[] = {8, 16, 24, 32};
+static const uint32_t kScalarNV[] = {16, 32};
+
+template <typename Elem, int EPV>
+static hipError_t launch_vec(const StepArgs &a, hipStream_t stream) {
+    switch (a.nv) {
+        case 8: return launch_pen<Elem, EPV, 8>(a, stream);
+        case 16: return launch_pen<Elem, EPV, 16>(a, stream);
+        case 24: return launch_pen<Elem, EPV, 24>(a, stream);
+        case 32: return launch_pen<Elem, EPV, 32>(a, stream);
+        case 40:
+            if constexpr (sizeof(Elem) == 2) return launch_pen<Elem, EPV, 40>(a, stream);
+            return hipErrorInvalidValue;
+        default: return hipErrorInvalidValue;
     }
-    if (pen == 2) return launch_one<Elem, EPV, VPL, false, 2>(a, stream);
-    if (pen == 1) return launch_one<Elem, EPV, VPL, false, 1>(a, stream);
-    return launch_one<Elem, EPV, VPL, false, 0>(a, stream);
+}
+
+template <typename Elem>
+static hipError_t launch_scalar(const StepArgs &a, hipStream_t stream) {
+    switch (a.nv) {
+        case 16: return launch_pen<Elem, 1, 16>(a, stream);
+        case 32: return launch_pen<Elem, 1, 32>(a, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <size_t N>
+static uint32_t pick_nv(const uint32_t (&list)[N], uint32_t need) {
+    for (uint32_t nv : list)
+        if (need <= nv) return nv;
+    return 0u;
+}
+
+uint32_t max_vectors_per_lane(uint32_t variant) {
+    switch (variant) {
+        case kVariantBf16Vec: return kBf16NV[4];
+        case kVariantF32Vec: return kF32NV[3];
+        default: return kScalarNV[1];
+    }
+}
+
+uint32_t vectors_per_lane(uint32_t variant, uint32_t need) {
+    switch (variant) {
+        case kVariantBf16Vec: return pick_nv(kBf16NV, need);
+        case kVariantF32Vec: return pick_nv(kF32NV, need);
+        default: return pick_nv(kScalarNV, need);
+    }
+}
+
+uint32_t bitmap_words_for(uint32_t variant, uint32_t vec_per_slice) {
+    const uint32_t epv = elems_per_vector(variant);
+    return slice_bitmap_words(vec_per_slice * epv, epv);
 }
 
 uint32_t elems_per_vector(uint32_t variant) {
@@ -1219,18 +1334,27 @@ uint32_t elems_per_vector(uint32_t variant) {
 uint32_t block_threads() { return (uint32_t)kBlock; }
 uint32_t merge_capacity() { return kCandCap; }
 
-// LDS use of the slice kernel (hash, bitmap, candidates, sorted list); the
-// launch computes the same sum.
-uint32_t stream_lds_bytes(uint32_t, bool, bool, uint32_t hash_slots, uint32_t bitmap_words, uint32_t kcap) {
-    return hash_slots * 4u + bitmap_words * 4u + kStreamCandCap * 8u + kcap * 8u;
+// LDS of the slice kernel, in its layout order: staged lane-vectors and their
+// slots, candidates, the sorted list, the history table, the penalty bitmap
+// and the mask bitmap.
+uint32_t stream_lds_bytes(uint32_t variant, bool mask, bool pen, uint32_t hash_slots, uint32_t bitmap_words,
+                          uint32_t kcap) {
+    uint32_t stage = 0;
+    switch (variant) {
+        case kVariantF32Vec: stage = stage_bytes<float, 4>(); break;
+        case kVariantBf16Vec: stage = stage_bytes<uint16_t, 8>(); break;
+        case kVariantF32Scalar: stage = stage_bytes<float, 1>(); break;
+        default: stage = stage_bytes<uint16_t, 1>(); break;
+    }
+    return stage + kStreamCandCap * 8u + kcap * 8u + hash_slots * 4u + bitmap_words * 4u * ((pen ? 1u : 0u) + (mask ? 1u : 0u));
 }
 
 hipError_t launch_sample_rows(uint32_t variant, const StepArgs &a, hipStream_t stream) {
     switch (variant) {
-        case kVariantF32Vec: return launch_variant<float, 4, 2>(a, stream);
-        case kVariantBf16Vec: return launch_variant<uint16_t, 8, 2>(a, stream);
-        case kVariantF32Scalar: return launch_variant<float, 1, 4>(a, stream);
-        case kVariantBf16Scalar: return launch_variant<uint16_t, 1, 4>(a, stream);
+        case kVariantF32Vec: return launch_vec<float, 4>(a, stream);
+        case kVariantBf16Vec: return launch_vec<uint16_t, 8>(a, stream);
+        case kVariantF32Scalar: return launch_scalar<float>(a, stream);
+        case kVariantBf16Scalar: return launch_scalar<uint16_t>(a, stream);
         default: return hipErrorInvalidValue;
     }
 }
