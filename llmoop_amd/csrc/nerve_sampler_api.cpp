@@ -332,6 +332,7 @@ int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *str
     if (pen || b->allowed) a.bitmap_words = nerve::bitmap_words_for(variant, vec_per_slice);
     uint32_t big = nerve::merge_capacity();
     if (slices * d.top_k_capacity > big) big = slices * d.top_k_capacity;
+    if (d.top_k_capacity + 32u > big) big = d.top_k_capacity + 32u;  // weights + running sums of the finish step
     a.big_entries = big;
     a.finish_lds_bytes = a.hash_slots * 4u + big * 8u + d.top_k_capacity * 8u;
     const uint32_t stream_lds = nerve::stream_lds_bytes(variant, b->allowed != nullptr, pen, a.hash_slots,

@@ -33,6 +33,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 #include "nerve_device_math.h"
 #include "nerve_sampler_internal.h"
 
@@ -40,11 +42,11 @@ namespace nerve {
 
 #ifdef NERVE_PHASE_TIMING
 // Profiling builds only: per-workgroup shader-clock stamps at phase boundaries.
-__device__ uint64_t g_phase_ts[16384 * 8];
+__device__ uint64_t g_phase_ts[16384 * 16];
 #define PHASE_MARK(i)                                                                        \
     do {                                                                                     \
         if (threadIdx.x == 0 && blockIdx.x < 16384u)                                         \
-            g_phase_ts[blockIdx.x * 8u + (i)] = __builtin_amdgcn_s_memtime();                \
+            g_phase_ts[blockIdx.x * 16u + (i)] = __builtin_amdgcn_s_memtime();               \
     } while (0)
 __device__ uint32_t g_dbg[16384 * 4];
 #define DBG_ADD(i, v) atomicAdd(&g_dbg[blockIdx.x * 4u + (i)], (v))
@@ -66,12 +68,40 @@ constexpr uint32_t kMaxHistory = NERVE_MAX_HISTORY_CAPACITY;
 
 __device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
 
+// Calls f(std::integral_constant<int, J>) for J = B .. E-1 in order: indices
+// into register arrays stay compile-time however large the body grows.
+template <int B, typename F, int... Js>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, Js...>) {
+    (f(std::integral_constant<int, B + Js>{}), ...);
+}
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (E > B) static_for_impl<B>(f, std::make_integer_sequence<int, E - B>{});
+}
+
 // Workgroup barrier that orders LDS only: waits for this wave's LDS traffic,
 // not for its global loads, so prefetched chunks stay in flight across it.
 __device__ __forceinline__ void lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// The largest t (top B bits significant, the rest zero) with at least `need`
+// of the wave's keys v[] >= t: an MSB-first search with ballot counts. 0 when
+// fewer than `need` keys are nonzero.
+template <int N, int B>
+__device__ __forceinline__ uint32_t wave_kth(const uint32_t (&v)[N], uint32_t need) {
+    uint32_t prefix = 0u;
+#pragma unroll
+    for (int b = 31; b >= 32 - B; --b) {
+        const uint32_t cand = prefix | (1u << b);
+        uint32_t cnt = 0u;
+#pragma unroll
+        for (int i = 0; i < N; ++i) cnt += (uint32_t)__popcll(__ballot(v[i] >= cand));
+        prefix = cnt >= need ? cand : prefix;
+    }
+    return prefix;
 }
 
 __device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
@@ -253,6 +283,7 @@ struct VecTraits<float, 4> {
     __device__ static __forceinline__ uint32_t merge(uint32_t a, uint32_t b) { return i32_max(a, b); }
     __device__ static __forceinline__ uint32_t report_bits(uint32_t acc, int) { return acc; }
     __device__ static __forceinline__ bool ge_pos(uint32_t vm, uint32_t thr) { return (int32_t)vm >= (int32_t)(thr & 0x7fffffffu); }
+    __device__ static __forceinline__ uint32_t staged_bits(const load_t *v, uint32_t i, uint32_t e) { return ((const uint32_t *)(v + i))[e]; }
     __device__ static __forceinline__ uint32_t upper(const load_t &r) {
         const uint32_t a = max(f32_key_upper(r[0]), f32_key_upper(r[1]));
         const uint32_t b = max(f32_key_upper(r[2]), f32_key_upper(r[3]));
@@ -280,6 +311,10 @@ struct VecTraits<uint16_t, 8> {
     __device__ static __forceinline__ bool ge_pos(uint32_t vm, uint32_t thr) {
         const int32_t m = max((int32_t)(int16_t)(vm & 0xffffu), (int32_t)(int16_t)(vm >> 16));
         return m >= (int32_t)(((thr & 0x7fffffffu) + 0xffffu) >> 16);
+    }
+    __device__ static __forceinline__ uint32_t staged_bits(const load_t *v, uint32_t i, uint32_t e) {
+        const uint32_t w = ((const uint32_t *)(v + i))[e >> 1];
+        return (e & 1u) ? (w & 0xffff0000u) : (w << 16);
     }
     __device__ static __forceinline__ uint32_t upper(const load_t &r) {
         const uint32_t m2 = u16x2_max(u16x2_max(bf16x2_keys(r[0]), bf16x2_keys(r[1])),
@@ -312,6 +347,7 @@ struct VecTraits<float, 1> {
     __device__ static __forceinline__ uint32_t merge(uint32_t a, uint32_t b) { return i32_max(a, b); }
     __device__ static __forceinline__ uint32_t report_bits(uint32_t acc, int) { return acc; }
     __device__ static __forceinline__ bool ge_pos(uint32_t vm, uint32_t thr) { return (int32_t)vm >= (int32_t)(thr & 0x7fffffffu); }
+    __device__ static __forceinline__ uint32_t staged_bits(const load_t *v, uint32_t i, uint32_t) { return f2u(v[i]); }
     __device__ static __forceinline__ uint32_t upper(const load_t &r) { return f32_key_upper(f2u(r)); }
     __device__ static __forceinline__ bool has_nan(const load_t &r) { return (f2u(r) & 0x7fffffffu) > 0x7f800000u; }
     __device__ static __forceinline__ uint32_t bits(const load_t &r, int) { return f2u(r); }
@@ -327,6 +363,7 @@ struct VecTraits<uint16_t, 1> {
     __device__ static __forceinline__ uint32_t merge(uint32_t a, uint32_t b) { return i32_max(a, b); }
     __device__ static __forceinline__ uint32_t report_bits(uint32_t acc, int) { return acc; }
     __device__ static __forceinline__ bool ge_pos(uint32_t vm, uint32_t thr) { return (int32_t)vm >= (int32_t)(thr & 0x7fffffffu); }
+    __device__ static __forceinline__ uint32_t staged_bits(const load_t *v, uint32_t i, uint32_t) { return (uint32_t)v[i] << 16; }
     __device__ static __forceinline__ uint32_t upper(const load_t &r) { return f32_key_upper((uint32_t)r << 16); }
     __device__ static __forceinline__ bool has_nan(const load_t &r) { return ((uint32_t)r & 0x7fffu) > 0x7f80u; }
     __device__ static __forceinline__ uint32_t bits(const load_t &r, int) { return (uint32_t)r << 16; }
@@ -339,7 +376,9 @@ struct RowCtx {
     const uint32_t *allowed_row;
     const uint32_t *seen_row;
     const uint32_t *hash;      // LDS
-    const uint32_t *bitmap;    // LDS (slice-relative) or null: probe the hash directly
+    // LDS bitmap of the slice's history ids (from tok0) with `hash` holding
+    // the occurrences beyond the first; or null, and `hash` holds full counts
+    const uint32_t *bitmap;
     uint32_t log2_slots;
     uint32_t tok0;
     float rep, freq, pres;
@@ -352,12 +391,12 @@ __device__ __forceinline__ float configured_at(const RowCtx &c, uint32_t t) {
     bool allowed = c.allowed_row ? ((c.allowed_row[t >> 5] >> (t & 31u)) & 1u) : true;
     uint32_t count = 0;
     if (c.history) {
-        bool bit = true;
         if (c.bitmap) {
-            uint32_t o = t - c.tok0;
-            bit = (c.bitmap[o >> 5] >> (o & 31u)) & 1u;
+            const uint32_t o = t - c.tok0;
+            if ((c.bitmap[o >> 5] >> (o & 31u)) & 1u) count = 1u + hash_lookup(c.hash, c.log2_slots, t);
+        } else {
+            count = hash_lookup(c.hash, c.log2_slots, t);
         }
-        if (bit) count = hash_lookup(c.hash, c.log2_slots, t);
     } else if (c.seen_row) {
         count = (c.seen_row[t >> 5] >> (t & 31u)) & 1u;
     }
@@ -503,6 +542,9 @@ struct SharedSmall {
     uint64_t red[kWaves];
     uint32_t flag[4];
     uint32_t ones[1];  // all-ones mask word of rows without a mask
+    uint32_t io[4];                  // the row's RowIo, stored during the set-up
+    uint32_t ukeys[2][kWaves * 64];  // report unions of the two threshold passes
+    uint32_t ucount[2][kWaves];
 };
 
 __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t n) {
@@ -513,6 +555,30 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t n) {
     return xcd < rem ? xcd * (q + 1u) + idx : rem * (q + 1u) + (xcd - rem) * q + idx;
 }
 
+// Per-row draw inputs, read at kernel start so their latency hides behind
+// the stream: the seed, the tick (stream control words 1-2, else the step),
+// and the output ring capacity (stream control word 4).
+struct RowIo {
+    uint32_t seed, tick_lo, tick_hi, ring_cap;
+};
+
+__device__ __forceinline__ RowIo load_row_io(const StepArgs &a, uint32_t row) {
+    RowIo io;
+    io.seed = a.seeds ? a.seeds[row] : 0u;
+    if (a.stream_control) {
+        const uint32_t *sc = a.stream_control + (uint64_t)row * 5u;
+        io.tick_lo = sc[1];
+        io.tick_hi = sc[2];
+        io.ring_cap = sc[4];
+    } else {
+        const uint64_t t = a.steps ? a.steps[row] : 0ull;
+        io.tick_lo = (uint32_t)t;
+        io.tick_hi = (uint32_t)(t >> 32);
+        io.ring_cap = 0u;
+    }
+    return io;
+}
+
 // Finishes one row from its sorted survivors s_sorted[0 .. n) (value desc,
 // id asc): EOS fallback for an all-zero mask, the greedy record (replaying the
 // reference's 1024-lane argmax when the row holds a NaN), or min-p / top-p over
@@ -521,13 +587,13 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t n) {
 // control tick and the output ring. Runs on NT threads; wave 0 does the
 // sequential running sums.
 template <typename Elem, int PEN, int NT>
-__device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, const nerve_sampler_row_params &P, uint32_t k,
+__device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, const RowIo &io, const nerve_sampler_row_params &P, uint32_t k,
                            bool sampled, uint32_t n, uint32_t row_flags, uint2 *s_sorted, uint2 *s_big,
                            uint32_t *s_hash, const RowCtx &ctx) {
     __shared__ uint32_t s_res[2];
     const uint32_t tid = threadIdx.x;
-    float *s_w = (float *)s_big;           // [kcap] weights
-    float *s_p = (float *)s_big + a.kcap;  // [kcap] running sums, then probabilities
+    float *s_w = (float *)s_big;                 // [kcap + 64] weights, zero past the min-p cut
+    float *s_p = (float *)s_big + a.kcap + 64u;  // [kcap] running sums, then probabilities
     uint32_t token = 0, sel_bits = 0, out_flags = 0, kout = 1;
     uint32_t *sc = a.stream_control ? a.stream_control + (uint64_t)row * 5u : nullptr;
 
@@ -595,6 +661,9 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
         if (tid < 64) {
             const uint32_t lane = tid;
             const float T = P.temperature;
+            // the uniform draw does not depend on the weights: start it first
+            const uint64_t tick = (uint64_t)io.tick_lo | ((uint64_t)io.tick_hi << 32);
+            const float u = random_unit(a.rng, io.seed, tick, row);
             const float l0 = entry_value(s_sorted[0]);
             const float m = l0 / T;
             float minimum = u2f(kLowestBits);
@@ -603,36 +672,35 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
                 const float d = T * lg;
                 minimum = l0 + d;
             }
-            // leading survivors not below the min-p floor
+            PHASE_MARK(13);
+            // Per chunk of 64 survivors: the min-p cut (the first survivor
+            // below the floor ends the list), the weights, and the running
+            // sums in the reference's sequential order: lane i adds w_c0,
+            // w_c0+1, ... in turn and +0.0 (exact) for the terms after its own,
+            // so its sum is the reference's prefix sum P_i, rounding for
+            // rounding. s_w is zero past the cut.
             uint32_t n_valid = k;
-            for (uint32_t c0 = 0; c0 < k; c0 += 64u) {
-                const uint32_t i = c0 + lane;
-                const uint64_t b = __ballot(i < k && entry_value(s_sorted[i]) < minimum);
-                if (b) {
-                    n_valid = c0 + (uint32_t)__builtin_ctzll(b);
-                    break;
-                }
-            }
-            // weights in parallel, running sums in the reference's sequential order
-            float acc = 0.0f;
+            float carry = 0.0f;  // P_(c0 - 1)
             for (uint32_t c0 = 0; c0 < n_valid; c0 += 64u) {
                 const uint32_t i = c0 + lane;
-                float w = 0.0f;
-                if (i < n_valid) {
-                    const float sc_ = entry_value(s_sorted[i]) / T;
-                    w = nerve_expf(sc_ - m);
-                    s_w[i] = w;
-                }
-                const uint32_t cnt = min(64u, n_valid - c0);
-                float mine = 0.0f;
-                for (uint32_t j = 0; j < cnt; ++j) {
-                    const float wj = __shfl(w, (int)j, 64);
-                    acc = acc + wj;
-                    if (lane == j) mine = acc;
-                }
-                if (i < n_valid) s_p[i] = mine;
+                const float v = i < k ? entry_value(s_sorted[i]) : 0.0f;
+                const uint64_t below = __ballot(i < k && v < minimum);
+                if (below) n_valid = min(n_valid, c0 + (uint32_t)__builtin_ctzll(below));
+                if (c0 >= n_valid) break;
+                const bool in = i < n_valid;
+                s_w[i] = in ? nerve_expf(v / T - m) : 0.0f;
+                PHASE_MARK(14);
+                float wv[64];
+                static_for<0, 64>([&](auto J) __attribute__((always_inline)) { wv[J] = s_w[c0 + (uint32_t)J]; });
+                float acc = carry;
+                static_for<0, 64>([&](auto J) __attribute__((always_inline)) {
+                    acc = acc + ((uint32_t)J <= lane ? wv[J] : 0.0f);
+                });
+                s_p[i] = acc;
+                carry = u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(min(64u, n_valid - c0) - 1u)));
             }
-            const float total = n_valid ? s_p[n_valid - 1u] : 0.0f;
+            PHASE_MARK(10);
+            const float total = n_valid ? carry : 0.0f;
             const float threshold = P.top_p * total;
             uint32_t nucleus = n_valid;
             for (uint32_t c0 = 0; c0 < n_valid; c0 += 64u) {
@@ -645,11 +713,7 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
             }
             if (nucleus == 0u) nucleus = 1u;
             const float nucleus_weight = n_valid ? s_p[nucleus - 1u] : 0.0f;
-            uint64_t tick;
-            if (sc) tick = (uint64_t)sc[1] | ((uint64_t)sc[2] << 32);
-            else tick = a.steps ? a.steps[row] : 0ull;
-            const uint32_t seed = a.seeds ? a.seeds[row] : 0u;
-            const float u = random_unit(a.rng, seed, tick, row);
+            PHASE_MARK(15);
             const float target = u * nucleus_weight;
             uint32_t selected = nucleus - 1u;
             for (uint32_t c0 = 0; c0 < nucleus && c0 < n_valid; c0 += 64u) {
@@ -668,6 +732,7 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
             }
         }
         __syncthreads();
+        PHASE_MARK(11);
         token = s_res[0];
         sel_bits = s_res[1];
         out_flags = NERVE_FLAG_SAMPLED;
@@ -683,10 +748,10 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
         o.reserved = 0u;
         a.out[row] = o;
         if (sc) {
-            const uint32_t lo = sc[1];
+            const uint32_t lo = io.tick_lo;
             if (a.ring) {
                 uint32_t *ring = a.ring + (uint64_t)row * a.ring_stride;
-                const uint32_t cap = sc[4];
+                const uint32_t cap = io.ring_cap;
                 ring[0] = token; ring[1] = sel_bits; ring[2] = out_flags; ring[3] = 0u;
                 if (cap) {
                     const uint64_t w = 4ull + (uint64_t)(lo % cap) * 4ull;
@@ -697,7 +762,7 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
             }
             sc[0] = token;
             const uint32_t next = lo + 1u;
-            if (next == 0u) sc[2] = sc[2] + 1u;
+            if (next == 0u) sc[2] = io.tick_hi + 1u;
             sc[1] = next;
         }
     }
@@ -724,6 +789,12 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
 
 constexpr uint32_t kStageCap = 1024;       // lane-vectors staged for exact work per slice
 constexpr uint32_t kStreamCandCap = 2048;  // candidate entries per slice
+
+// Bytes of the staging area (lane-vectors and their slots).
+template <typename Elem, int EPV>
+__host__ __device__ constexpr uint32_t stage_area_bytes() {
+    return kStageCap * ((uint32_t)sizeof(typename VecTraits<Elem, EPV>::load_t) + 4u);
+}
 
 // Bitmap words of a slice: its tokens [tok0, tok1) rounded out to 32-token
 // words, plus slack; the host sizes the LDS bitmaps with the same bound.
@@ -761,12 +832,12 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     constexpr uint32_t kVecBytes = (uint32_t)sizeof(vec_t);
     __shared__ SharedSmall sm;
     extern __shared__ __align__(16) uint32_t s_dyn[];
-    vec_t *s_svec = (vec_t *)s_dyn;                                // [kStageCap]
+    uint32_t *s_hash = s_dyn;                                      // [hash_slots], a multiple of 64
+    vec_t *s_svec = (vec_t *)(s_hash + a.hash_slots);              // [kStageCap]
     uint32_t *s_sslot = (uint32_t *)(s_svec + kStageCap);          // [kStageCap]
     uint2 *s_cand = (uint2 *)(s_sslot + kStageCap);                // [kStreamCandCap], later finish scratch
     uint2 *s_sorted = s_cand + kStreamCandCap;                     // [kcap]
-    uint32_t *s_hash = (uint32_t *)(s_sorted + a.kcap);            // [hash_slots]
-    uint32_t *s_pen = s_hash + a.hash_slots;                       // [bitmap_words] when PEN != 0
+    uint32_t *s_pen = (uint32_t *)(s_sorted + a.kcap);             // [bitmap_words] when PEN != 0
     uint32_t *s_allow = s_pen + (PEN != 0 ? a.bitmap_words : 0u);  // [bitmap_words] with a mask
     uint2 *s_big = s_cand;
 
@@ -776,6 +847,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     const uint32_t slice = logical % a.slices;
 
     const nerve_sampler_row_params P = a.params[row];
+    const RowIo io = a.slices == 1u ? load_row_io(a, row) : RowIo{0u, 0u, 0u, 0u};
     const bool sampled = P.method != NERVE_METHOD_GREEDY;
     uint32_t k = sampled ? P.top_k : 1u;
     k = k < 1u ? 1u : (k > a.kcap ? a.kcap : k);
@@ -801,12 +873,16 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
 
     PHASE_MARK(0);
     // 1. loads: history ids and bitmap words first (they are needed first),
-    // then the first half of the slice's lane-vectors through a buffer
-    // resource bounded by v1 (a slot past the slice reads as zero and is never
-    // used). A wave owns 64 * NV consecutive slots, so the loads of a lane sit
-    // 64 slots apart and share one offset register per 4 KiB.
+    // then the first D lane-vectors through a buffer resource bounded by v1
+    // (a slot past the slice reads as zero and is never used). A wave owns
+    // 64 * NV consecutive slots, so the loads of a lane sit 64 slots apart and
+    // share one offset register per 4 KiB.
     const uint32_t lane = lane_id();
-    const uint32_t wbase = (tid >> 6) * 64u * (uint32_t)NV + lane;  // slot of lane-vector 0, relative to v0
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // the slice is spread evenly: wave w owns `span` slots from w * span
+    const uint32_t span = ((a.vec_per_slice + (uint32_t)kBlock - 1u) / (uint32_t)kBlock) * 64u;
+    const uint32_t wslots = v1 - v0 > wave * span ? min(span, v1 - v0 - wave * span) : 0u;  // valid slots of the wave
+    const uint32_t wbase = wave * span + lane;  // slot of lane-vector 0, relative to v0
     uint32_t hist[history ? HPT : 1];
     uint32_t hlen = 0;
     if constexpr (history) {
@@ -827,29 +903,42 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
 #pragma unroll
         for (int i = 0; i < BW; ++i) sw[i] = srow[(bm_base >> 5) + min(tid + (uint32_t)i * kBlock, bm_last)];
     }
+    // per-wave buffer resource: a load past the wave's valid run reads zero
+    // and costs no memory traffic
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(lrow + (uint64_t)v0 * EPV), (short)0, (int)((v1 - v0) * kVecBytes), 0x00020000);
+        (void *)(lrow + (uint64_t)(v0 + wave * span) * EPV), (short)0, (int)(wslots * kVecBytes), 0x00020000);
     vec_t data[NV];
     auto load = [&](int j) __attribute__((always_inline)) {
-        const uint32_t off = (wbase + (uint32_t)j * 64u) * kVecBytes;
+        const uint32_t off = (lane + (uint32_t)j * 64u) * kVecBytes;
         if constexpr (kVecBytes == 16) data[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
         else if constexpr (kVecBytes == 4) data[j] = u2f(__builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, 0));
         else data[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
     };
-    constexpr int NA = NV / 2;  // issued before the LDS set-up, the rest after it
-#pragma unroll
-    for (int j = 0; j < NA; ++j) load(j);
+    // lane-vectors in flight ahead of the one being processed
+#ifndef NERVE_LOOKAHEAD
+#define NERVE_LOOKAHEAD 16
+#endif
+    constexpr int D = NV < NERVE_LOOKAHEAD ? NV : NERVE_LOOKAHEAD;
+    static_for<0, D>([&](auto J) __attribute__((always_inline)) { load(J); });
+    PHASE_MARK(1);
 
     // 2. LDS state: counters, mask / seen words of the slice (bits outside
-    // [tok0, tok1) cleared), history ids -> bitmap + id -> count table
+    // [tok0, tok1) cleared); history ids -> bitmap, and repeats -> a table of
+    // occurrences beyond the first
     if constexpr (history) {
-        for (uint32_t i = tid; i < a.hash_slots; i += kBlock) s_hash[i] = kHashEmpty;
+        const uint4 empty4 = make_uint4(kHashEmpty, kHashEmpty, kHashEmpty, kHashEmpty);
+        for (uint32_t i = tid; i < a.hash_slots / 4u; i += kBlock) ((uint4 *)s_hash)[i] = empty4;
         for (uint32_t i = tid; i < bm_n; i += kBlock) s_pen[i] = 0u;
     }
     if (tid == 0) {
         sm.flag[1] = 0u;  // candidates
         sm.flag[2] = 0u;  // staged lane-vectors
+        sm.flag[3] = 0u;  // slice flags
         sm.ones[0] = 0xffffffffu;
+        sm.io[0] = io.seed;
+        sm.io[1] = io.tick_lo;
+        sm.io[2] = io.tick_hi;
+        sm.io[3] = io.ring_cap;
     }
     auto range_bits = [&](uint32_t w) __attribute__((always_inline)) -> uint32_t {
         const uint32_t t = bm_base + w * 32u;
@@ -879,87 +968,134 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     }
     lds_sync();
     if constexpr (history) {
+        uint32_t first[HPT];
 #pragma unroll
         for (int h = 0; h < HPT; ++h) {
             const uint32_t id = hist[h];
+            first[h] = 0xffffffffu;
             if (tid + (uint32_t)h * kBlock < hlen && id >= tok0 && id < tok1) {
                 const uint32_t o = id - bm_base;
-                atomicOr(&s_pen[o >> 5], 1u << (o & 31u));
-                hash_insert(s_hash, a.log2_slots, id);
+                first[h] = atomicOr(&s_pen[o >> 5], 1u << (o & 31u)) & (1u << (o & 31u));
             }
         }
-    }
 #pragma unroll
-    for (int j = NA; j < NV; ++j) load(j);
-    if constexpr (history) lds_sync();
-    PHASE_MARK(1);
+        for (int h = 0; h < HPT; ++h)
+            if (first[h] != 0xffffffffu && first[h] != 0u) hash_insert(s_hash, a.log2_slots, hist[h]);
+        lds_sync();
+    }
+    PHASE_MARK(2);
 
-    // 3. pass 1: lane reports from lane-vectors whose every element is valid,
-    // allowed and free of penalty state
-    const uint32_t nval = v1 - v0 > wbase ? (v1 - v0 - wbase + 63u) / 64u : 0u;  // valid lane-vectors of this lane
+    // 3. the stream. Lane-vector j is processed as it lands while lane-vector
+    // j + D is issued. Per group of 8: the flags from the LDS bitmaps (ok =
+    // every element valid, allowed and free of penalty state; live = some
+    // element valid and allowed). Pass 1 folds ok lane-vectors into the lane
+    // reports. After the first half, thr (a lower bound of the slice's k-th
+    // largest key, from the reports so far) is set and pass 2 stages every
+    // lane-vector that can hold a key >= thr, first-half ones included.
+    const uint32_t nval = wslots > lane ? (wslots - lane + 63u) / 64u : 0u;  // valid lane-vectors of this lane
     const uint32_t *mask_words = mask ? s_allow : sm.ones;
-    // 1a: per lane-vector flags as bit masks (ok = every element valid,
-    // allowed and free of penalty state; live = some element valid and allowed)
+    const uint32_t idx_mask = mask ? 0xffffffffu : 0u;  // rows without a mask read an all-ones word
+    const bool need_bits = mask || PEN != 0;
     uint32_t okm[LW], live[LW];
 #pragma unroll
     for (int i = 0; i < LW; ++i) {
-        okm[i] = 0u;
-        live[i] = 0u;
+        const uint32_t lo = (uint32_t)i * 32u;
+        const uint32_t n = nval > lo ? min(nval - lo, 32u) : 0u;
+        okm[i] = n >= 32u ? 0xffffffffu : ((1u << n) - 1u);  // valid lane-vectors
+        live[i] = okm[i];
     }
+    auto flags_group = [&](int j0, int j1) __attribute__((always_inline)) {
+        uint32_t aw[8], pw[8], sh[8];
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const bool valid = (uint32_t)j < nval;
-        uint32_t okb = valid ? kFull : 0u, anyb = okb;
-        {
-            // branch-free: a row without a mask reads an all-ones word
-            const uint32_t off = valid ? (v0 + wbase + (uint32_t)j * 64u) * EPV - bm_base : 0u;
-            const uint32_t ab = (mask_words[mask ? off >> 5 : 0u] >> (mask ? off & 31u : 0u)) & kFull;
-            okb &= ab;
-            anyb &= ab;
-            if constexpr (PEN != 0) okb = ((s_pen[off >> 5] >> (off & 31u)) & kFull) ? 0u : okb;
+        for (int j = j0; j < j1; ++j) {
+            const uint32_t off = (uint32_t)j < nval ? (v0 + wbase + (uint32_t)j * 64u) * EPV - bm_base : 0u;
+            sh[j - j0] = off & 31u;
+            aw[j - j0] = mask_words[(off >> 5) & idx_mask];
+            if constexpr (PEN != 0) pw[j - j0] = s_pen[off >> 5];
         }
-        okm[j >> 5] |= (okb == kFull ? 1u : 0u) << (j & 31);
-        live[j >> 5] |= (anyb ? 1u : 0u) << (j & 31);
-        // bound how far the bitmap reads are hoisted: each holds a VGPR
-        // while the whole slice is already resident
-        if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-    }
-    // 1b: the two report accumulators, in load order
-    uint32_t acc0 = VT::kAccInit, acc1 = VT::kAccInit;
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
+        for (int j = j0; j < j1; ++j) {
+            const uint32_t valid = (okm[j >> 5] >> (j & 31)) & 1u ? kFull : 0u;
+            const uint32_t ab = (aw[j - j0] >> (mask ? sh[j - j0] : 0u)) & valid;
+            uint32_t okb = ab;
+            if constexpr (PEN != 0) okb = ((pw[j - j0] >> sh[j - j0]) & kFull) ? 0u : okb;
+            const uint32_t bit = 1u << (j & 31);
+            okm[j >> 5] = okb == kFull ? (okm[j >> 5] | bit) : (okm[j >> 5] & ~bit);
+            live[j >> 5] = ab ? (live[j >> 5] | bit) : (live[j >> 5] & ~bit);
+        }
+    };
+    uint32_t acc0 = VT::kAccInit, acc1 = VT::kAccInit;
+    auto pass1 = [&](int j) __attribute__((always_inline)) {
         const uint32_t vm = VT::vmax(data[j]);
         const bool ok = (okm[j >> 5] >> (j & 31)) & 1u;
         if (j & 1) acc1 = ok ? VT::merge(acc1, vm) : acc1;
         else acc0 = ok ? VT::merge(acc0, vm) : acc0;
-    }
-
-    // 4. thr = the k-th largest report key (1 when fewer than k reports)
-    constexpr int NR = 2 * VT::kReports;
-    uint32_t rep[NR];
+        // pass 2 recomputes the maximum: keeping this one alive until then
+        // would cost a VGPR per lane-vector
+        asm volatile("" : "+v"(data[j]));
+    };
+    // Threshold from the reports. Every wave finds the 64th largest of its own
+    // report keys (an MSB-first ballot search over the top key bits) and
+    // appends its reports at or above it to an LDS union (at most 64 per
+    // wave); every wave then takes the k-th largest of the union the same way.
+    // Union members are real elements of the slice, so at least k keys reach
+    // the result, and for k <= 64 it is the k-th largest report (to the
+    // searched bits). 1 when the union has fewer than k.
+    auto report_threshold = [&](int call) __attribute__((always_inline)) -> uint32_t {
+        constexpr int NR = 2 * VT::kReports;
+        constexpr int kBits = sizeof(Elem) == 2 ? 16 : 24;
+        uint32_t rep[NR];
 #pragma unroll
-    for (int r = 0; r < VT::kReports; ++r) {
-        const uint32_t b0 = VT::report_bits(acc0, r), b1 = VT::report_bits(acc1, r);
-        uint32_t k0 = b0 == 0x80000000u ? 0u : raw_order_key(b0);
-        uint32_t k1 = b1 == 0x80000000u ? 0u : raw_order_key(b1);
-        rep[2 * r] = k0 < valid_min ? 0u : k0;
-        rep[2 * r + 1] = k1 < valid_min ? 0u : k1;
-    }
-    uint32_t unused_count;
-    uint32_t thr = radix_threshold<NR>(rep, k, sizeof(Elem) == 2 ? 2 : 3, sm.hist, sm.sel, unused_count);
-    thr = thr < 1u ? 1u : thr;
-    PHASE_MARK(2);
-
-    // Pass 2 recomputes the lane-vector maxima: keeping the pass-1 values
-    // alive would cost NV more VGPRs than the slice can spare.
+        for (int r = 0; r < VT::kReports; ++r) {
+            const uint32_t b0 = VT::report_bits(acc0, r), b1 = VT::report_bits(acc1, r);
+            const uint32_t k0 = b0 == 0x80000000u ? 0u : raw_order_key(b0);
+            const uint32_t k1 = b1 == 0x80000000u ? 0u : raw_order_key(b1);
+            rep[2 * r] = k0 < valid_min ? 0u : k0;
+            rep[2 * r + 1] = k1 < valid_min ? 0u : k1;
+        }
+        const uint32_t tw = wave_kth<NR, kBits>(rep, 64u);
+        uint32_t n = 0u;
+        uint32_t *u = sm.ukeys[call] + wave * 64u;
 #pragma unroll
-    for (int j = 0; j < NV; ++j) asm volatile("" : "+v"(data[j]));
-
-    // 5. pass 2: stage the lane-vectors that can hold a key >= thr. Masked
-    // lane-vectors are skipped unless a masked token could still qualify
-    // (greedy rows treat masked tokens as -inf).
-    const bool skip_dead = sampled || thr > kNegInfKey;
-    auto stage = [&](int j, bool go) __attribute__((always_inline)) {
+        for (int r = 0; r < NR; ++r) {
+            const bool in = rep[r] != 0u && rep[r] >= tw;
+            const uint64_t b = __ballot(in);
+            const uint32_t pos = n + __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+            if (in && pos < 64u) u[pos] = rep[r];
+            n += (uint32_t)__popcll(b);
+        }
+        if (lane == 0u) sm.ucount[call][wave] = min(n, 64u);
+        lds_sync();
+        uint32_t uk[kWaves];
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) uk[w] = lane < sm.ucount[call][w] ? sm.ukeys[call][w * 64 + lane] : 0u;
+        const uint32_t t = wave_kth<kWaves, kBits>(uk, k);
+        return t < 1u ? 1u : t;
+    };
+    uint32_t thr = 1u;
+    bool fast = false, skip_dead = true;
+    // Masked lane-vectors are skipped unless a masked token could still
+    // qualify (greedy rows treat masked tokens as -inf); a positive thr is
+    // tested on the raw signed-integer maximum.
+    auto set_thr = [&](uint32_t t) __attribute__((always_inline)) {
+        thr = t;
+        fast = thr > kZeroKey;
+        skip_dead = sampled || thr > kNegInfKey;
+    };
+    uint32_t has_nan = 0u;  // greedy rows: any NaN selects the reference's lane-structure replay
+    // Pass 2 for lane-vector j with the threshold test fixed at compile time:
+    // FAST for thr above +0 (raw signed-integer maximum), else the order-key
+    // upper bound.
+    auto pass2 = [&](auto fast_tag, int j) __attribute__((always_inline)) {
+        constexpr bool FAST = decltype(fast_tag)::value;
+        if (!sampled) has_nan |= ((uint32_t)j < nval && VT::has_nan(data[j])) ? 1u : 0u;
+        bool go;
+        if constexpr (FAST) {
+            go = ((live[j >> 5] >> (j & 31)) & 1u) && VT::ge_pos(VT::vmax(data[j]), thr);
+        } else {
+            const bool lv = skip_dead ? ((live[j >> 5] >> (j & 31)) & 1u) : ((uint32_t)j < nval);
+            go = lv && VT::upper(data[j]) >= thr;
+        }
         if (go) {
             const uint32_t pos = atomicAdd(&sm.flag[2], 1u);
             if (pos < kStageCap) {
@@ -967,39 +1103,77 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
                 s_sslot[pos] = v0 + wbase + (uint32_t)j * 64u;
             }
         }
+        asm volatile("" : "+v"(data[j]));  // as in pass 1: no maximum kept alive
     };
-    if (thr > kZeroKey) {
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const bool lv = skip_dead ? ((live[j >> 5] >> (j & 31)) & 1u) : ((uint32_t)j < nval);
-            stage(j, lv && VT::ge_pos(VT::vmax(data[j]), thr));
+    constexpr int NA = NV / 2;
+    static_assert(NV % 8 == 0, "lane-vector count must be a multiple of 8");
+    auto step_in = [&](auto J) __attribute__((always_inline)) {
+        constexpr int j = J;
+        if constexpr (j + D < NV) load(j + D);
+        if constexpr ((j & 7) == 0) {
+            if (need_bits) flags_group(j, j + 8);
         }
-    } else {
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const bool lv = skip_dead ? ((live[j >> 5] >> (j & 31)) & 1u) : ((uint32_t)j < nval);
-            stage(j, lv && VT::upper(data[j]) >= thr);
-        }
-    }
+        pass1(j);
+    };
+    static_for<0, NA>(step_in);
+    set_thr(report_threshold(0));
+    PHASE_MARK(4);
+    auto second_half = [&](auto fast_tag) __attribute__((always_inline)) {
+        static_for<NA, NV>([&](auto J) __attribute__((always_inline)) {
+            step_in(J);
+            pass2(fast_tag, J - NA);
+            pass2(fast_tag, J);
+        });
+    };
+    if (fast) second_half(std::true_type{});
+    else second_half(std::false_type{});
     // the V % EPV tail of the last slice, one element per lane (loaded late:
-    // it is rare and holding it across the passes costs a VGPR)
+    // it is rare and holding it across the stream costs a VGPR)
     const uint32_t tail_bits = has_tail ? f2u(load_elem<Elem>(lrow, tail_id)) : 0u;
-    // greedy rows: any NaN selects the reference's lane-structure replay
-    uint32_t has_nan = 0u;
     if (!sampled) {
-#pragma unroll
-        for (int j = 0; j < NV; ++j) has_nan |= ((uint32_t)j < nval && VT::has_nan(data[j])) ? 1u : 0u;
         if (has_tail) has_nan |= ((tail_bits & 0x7fffffffu) > 0x7f800000u) ? 1u : 0u;
         const float pq = P.repetition_penalty + P.frequency_penalty + P.presence_penalty;
         if (PEN != 0 && !(pq - pq == 0.0f)) has_nan = 1u;  // non-finite penalty parameters
     }
-    PHASE_MARK(3);
+    lds_sync();
+    uint32_t nstaged = sm.flag[2];
+    if (nstaged > kStageCap) {
+        // The first half's threshold let too much through (a skewed row):
+        // take the threshold of every report and stage again, reloading the
+        // slice in chunks of 8 lane-vectors (the registers were released as
+        // the stream went).
+        set_thr(report_threshold(1));
+        if (tid == 0) sm.flag[2] = 0u;
+        lds_sync();
+        constexpr int CH = 8;
+        auto restage = [&](auto fast_tag) __attribute__((always_inline)) {
+            static_for<0, NV / CH>([&](auto C) __attribute__((always_inline)) {
+                constexpr int j0 = C * CH, j1 = j0 + CH;
+                static_for<j0, j1>([&](auto J) __attribute__((always_inline)) { load(J); });
+                static_for<j0, j1>([&](auto J) __attribute__((always_inline)) { pass2(fast_tag, J); });
+            });
+        };
+        if (fast) restage(std::true_type{});
+        else restage(std::false_type{});
+        lds_sync();
+        nstaged = sm.flag[2];
+    } else if (nstaged > 128u && nstaged > 2u * k) {
+        // a weak first-half threshold: refine it from every report before
+        // the exact pass (the staged set stays a superset)
+        const uint32_t t = report_threshold(1);
+        if (t > thr) set_thr(t);
+    }
+    PHASE_MARK(5);
 
-    // 6. exact keys of the staged lane-vectors, the tail, and (for penalties
-    // that may raise a logit) every penalised token from the history state
+    // 5. exact keys of the staged elements (one lane per element), the tail,
+    // and (for penalties that may raise a logit) every penalised token from
+    // the history state
     auto push = [&](uint32_t key, uint32_t id) __attribute__((always_inline)) {
         const uint32_t pos = atomicAdd(&sm.flag[1], 1u);
         if (pos < kStreamCandCap) s_cand[pos] = make_uint2(key, id);
+    };
+    auto count_of = [&](uint32_t id) __attribute__((always_inline)) -> uint32_t {
+        return history ? 1u + hash_lookup(s_hash, a.log2_slots, id) : 1u;
     };
     auto pen_key = [&](uint32_t bits, bool allowed, uint32_t count) __attribute__((always_inline)) -> uint32_t {
         if (!allowed) return masked_key;
@@ -1008,56 +1182,80 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         const uint32_t key = order_key(v);
         return key < valid_min ? 0u : key;
     };
-    auto exact_elem = [&](uint32_t bits, uint32_t id) __attribute__((always_inline)) {
+    // configured key of a token from the vector passes (0: not a candidate;
+    // penalised tokens under raising penalties are left to the history pass)
+    auto elem_key = [&](uint32_t bits, uint32_t id) __attribute__((always_inline)) -> uint32_t {
         const uint32_t off = id - bm_base;
         const bool allowed = !mask || ((s_allow[off >> 5] >> (off & 31u)) & 1u);
         bool pen = false;
         if constexpr (PEN != 0) pen = (s_pen[off >> 5] >> (off & 31u)) & 1u;
-        uint32_t key;
-        if (pen) {
-            if (!lowering) return;  // evaluated from the history state below
-            key = pen_key(bits, allowed, history ? hash_lookup(s_hash, a.log2_slots, id) : 1u);
-        } else {
-            key = allowed ? raw_order_key(bits) : masked_key;
-            key = key < valid_min ? 0u : key;
-        }
-        if (key >= thr && key != 0u) push(key, id);
+        if (pen) return lowering ? pen_key(bits, allowed, count_of(id)) : 0u;
+        const uint32_t key = allowed ? raw_order_key(bits) : masked_key;
+        return key < valid_min ? 0u : key;
     };
-    if (has_tail) exact_elem(tail_bits, tail_id);
-    lds_sync();
-    const uint32_t nstaged = sm.flag[2];
-    if (nstaged <= kStageCap) {
-        for (uint32_t i = tid; i < nstaged; i += kBlock) {
-            const vec_t vec = s_svec[i];
-            const uint32_t id0 = s_sslot[i] * EPV;
-#pragma unroll
-            for (int e = 0; e < EPV; ++e) exact_elem(VT::bits(vec, e), id0 + (uint32_t)e);
+    constexpr uint32_t kLog2Epv = EPV == 8 ? 3u : (EPV == 4 ? 2u : 0u);
+    auto staged_key = [&](uint32_t q) __attribute__((always_inline)) -> uint32_t {
+        const uint32_t i = q >> kLog2Epv, e = q & (uint32_t)(EPV - 1);
+        return elem_key(VT::staged_bits(s_svec, i, e), s_sslot[i] * EPV + e);
+    };
+    auto push_staged = [&]() __attribute__((always_inline)) {
+        if (has_tail) {
+            const uint32_t key = elem_key(tail_bits, tail_id);
+            if (key >= thr && key != 0u) push(key, tail_id);
         }
+        for (uint32_t q = tid; q < (nstaged << kLog2Epv); q += kBlock) {
+            const uint32_t key = staged_key(q);
+            if (key >= thr && key != 0u) push(key, s_sslot[q >> kLog2Epv] * EPV + (q & (uint32_t)(EPV - 1)));
+        }
+    };
+    if (nstaged > kStageCap) {
+        if (has_tail) {
+            const uint32_t key = elem_key(tail_bits, tail_id);
+            if (key >= thr && key != 0u) push(key, tail_id);
+        }
+    } else {
+        push_staged();
         if (PEN != 0 && !lowering) {
-            auto pen_token = [&](uint32_t id, uint32_t count) __attribute__((always_inline)) {
-                const uint32_t off = id - bm_base;
-                const bool allowed = !mask || ((s_allow[off >> 5] >> (off & 31u)) & 1u);
-                const uint32_t key = pen_key(f2u(load_elem<Elem>(lrow, id)), allowed, count);
-                if (key >= thr && key != 0u) push(key, id);
-            };
-            if constexpr (history) {
-                for (uint32_t i = tid; i < a.hash_slots; i += kBlock) {
-                    const uint32_t cur = s_hash[i];
-                    if (cur != kHashEmpty) pen_token(cur >> 12, cur & 0xfffu);
-                }
-            } else if constexpr (PEN == 1) {
-                for (uint32_t w = tid; w < bm_n; w += kBlock) {
-                    uint32_t bits = s_pen[w];
-                    while (bits) {
-                        const uint32_t b = (uint32_t)__builtin_ctz(bits);
-                        bits &= bits - 1u;
-                        pen_token(bm_base + w * 32u + b, 1u);
-                    }
+            for (uint32_t w = tid; w < bm_n; w += kBlock) {
+                uint32_t bits = s_pen[w];
+                while (bits) {
+                    const uint32_t b = (uint32_t)__builtin_ctz(bits);
+                    bits &= bits - 1u;
+                    const uint32_t id = bm_base + w * 32u + b;
+                    const uint32_t off = id - bm_base;
+                    const bool allowed = !mask || ((s_allow[off >> 5] >> (off & 31u)) & 1u);
+                    const uint32_t key = pen_key(f2u(load_elem<Elem>(lrow, id)), allowed, count_of(id));
+                    if (key >= thr && key != 0u) push(key, id);
                 }
             }
         }
     }
+    {
+        // slice flags: bit 0 = some token allowed, bit 1 = greedy row holds a NaN
+        const uint32_t f = (__ballot(any_allowed != 0u) ? 1u : 0u) | (__ballot(has_nan != 0u) ? 2u : 0u);
+        if (lane == 0u && f) atomicOr(&sm.flag[3], f);
+    }
     lds_sync();
+    const uint32_t flags_slice = sm.flag[3];
+    if (nstaged <= kStageCap && sm.flag[1] > kStreamCandCap && (PEN == 0 || lowering)) {
+        // Too many candidates for a weak threshold: the exact k-th key of the
+        // staged elements (plus the tail) is a threshold that keeps at least k.
+        lds_sync();
+        const uint32_t n_el = (nstaged << kLog2Epv) + (last_slice ? (uint32_t)(a.vocab - nfull * EPV) : 0u);
+        auto any_key = [&](uint32_t q) __attribute__((always_inline)) -> uint32_t {
+            if (q < (nstaged << kLog2Epv)) return staged_key(q);
+            const uint32_t t = nfull * EPV + (q - (nstaged << kLog2Epv));
+            return elem_key(f2u(load_elem<Elem>(lrow, t)), t);
+        };
+        uint32_t unused_count;
+        const uint32_t t = radix_threshold_fn(0u, n_el, k, sm.hist, sm.sel, unused_count, any_key);
+        set_thr(t > thr ? t : thr);
+        if (tid == 0) sm.flag[1] = 0u;
+        lds_sync();
+        push_staged();
+        lds_sync();
+    }
+    PHASE_MARK(6);
 
     RowCtx ctx;
     ctx.logits_row = lrow;
@@ -1072,13 +1270,15 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     ctx.pres = P.presence_penalty;
     ctx.history = history;
 
-    // slice flags: bit 0 = some token allowed, bit 1 = greedy row holds a NaN
-    const uint32_t fsum = block_sum(any_allowed | (has_nan << 16), sm.scan);
-    const uint32_t flags_slice = ((fsum & 0xffffu) ? 1u : 0u) | ((fsum >> 16) ? 2u : 0u);
-    PHASE_MARK(4);
+    PHASE_MARK(7);
 
     // 7. selection -> s_sorted[0 .. n_out)
     uint32_t C = sm.flag[1];
+    if (tid == 0) {
+        DBG_SET(0, nstaged);
+        DBG_SET(1, C);
+        DBG_SET(2, thr);
+    }
     if (nstaged > kStageCap || C > kStreamCandCap) {
         // Skewed slice (for example a constant row): exact selection recomputed
         // from memory. The k-th largest key kv, then the `need` smallest ids
@@ -1108,24 +1308,57 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         lds_sync();
         C = min(sm.flag[1], kStreamCandCap);
     }
-    // rank sort (ids are distinct, so ranks are a permutation)
-    for (uint32_t i = tid; i < C; i += kBlock) {
-        const uint2 e = s_cand[i];
-        uint32_t r0 = 0, r1 = 0, r2 = 0, r3 = 0;
-        uint32_t j = 0;
-        for (; j + 4u <= C; j += 4u) {
-            r0 += entry_better(s_cand[j], e) ? 1u : 0u;
-            r1 += entry_better(s_cand[j + 1u], e) ? 1u : 0u;
-            r2 += entry_better(s_cand[j + 2u], e) ? 1u : 0u;
-            r3 += entry_better(s_cand[j + 3u], e) ? 1u : 0u;
+    // Many candidates (a weak threshold): keep the entries at or above the
+    // k-th largest key (LDS radix select) in the staging area, which is free
+    // by now, so the rank sort below stays small.
+    const uint2 *list = s_cand;
+    constexpr uint32_t kTrimCap = stage_area_bytes<Elem, EPV>() / 8u;
+    if (C > 256u && C > 4u * k) {
+        auto cand_key = [&](uint32_t i) __attribute__((always_inline)) -> uint32_t { return s_cand[i].x; };
+        uint32_t unused_count;
+        const uint32_t kth = radix_threshold_fn(0u, C, k, sm.hist, sm.sel, unused_count, cand_key);
+        uint2 *s_trim = (uint2 *)s_svec;
+        if (tid == 0) sm.flag[0] = 0u;
+        lds_sync();
+        for (uint32_t i = tid; i < C; i += kBlock) {
+            const uint2 e = s_cand[i];
+            if (e.x >= kth) {
+                const uint32_t q = atomicAdd(&sm.flag[0], 1u);
+                if (q < kTrimCap) s_trim[q] = e;
+            }
         }
-        for (; j < C; ++j) r0 += entry_better(s_cand[j], e) ? 1u : 0u;
-        const uint32_t r = r0 + r1 + r2 + r3;
-        if (r < k) s_sorted[r] = e;
+        lds_sync();
+        if (sm.flag[0] <= kTrimCap) {
+            list = s_trim;
+            C = sm.flag[0];
+        }
+    }
+    // rank sort (ids are distinct, so ranks are a permutation): G adjacent
+    // lanes share a candidate, each counting the better entries in every G-th
+    // position, and the partial ranks are summed across the group
+    uint32_t G = 1u;
+    while (G < 8u && C * G * 2u <= (uint32_t)kBlock) G <<= 1;
+    for (uint32_t base = 0; base < C * G; base += kBlock) {
+        const uint32_t q = base + tid, i = q / G, part = q % G;
+        uint32_t r = 0;
+        uint2 e = make_uint2(0u, 0u);
+        if (i < C) {
+            e = list[i];
+            uint32_t r1 = 0;
+            uint32_t j = part;
+            for (; j + G < C; j += 2u * G) {
+                r += entry_better(list[j], e) ? 1u : 0u;
+                r1 += entry_better(list[j + G], e) ? 1u : 0u;
+            }
+            if (j < C) r += entry_better(list[j], e) ? 1u : 0u;
+            r += r1;
+        }
+        for (uint32_t o = 1u; o < G; o <<= 1) r += __shfl_xor(r, (int)o, 64);
+        if (i < C && part == 0u && r < k) s_sorted[r] = e;
     }
     const uint32_t n_out = C < k ? C : k;
     lds_sync();
-    PHASE_MARK(5);
+    PHASE_MARK(8);
 
     // the sign of a zero survivor comes from its own configured value
     for (uint32_t i = tid; i < n_out; i += kBlock) {
@@ -1136,7 +1369,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         }
     }
     __syncthreads();
-    PHASE_MARK(6);
+    PHASE_MARK(9);
 
     // 8. publish: with several slices the sorted list goes to scratch and the
     // finish kernel merges the row; a single slice finishes here.
@@ -1144,10 +1377,12 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         uint2 *lists = a.scratch_lists + (uint64_t)(row * a.slices + slice) * a.kcap;
         for (uint32_t i = tid; i < n_out; i += kBlock) lists[i] = s_sorted[i];
         if (tid == 0) a.scratch_meta[row * a.slices + slice] = n_out | (flags_slice << 16);
-        PHASE_MARK(7);
+        PHASE_MARK(12);
         return;
     }
-    finish_row<Elem, PEN, kBlock>(a, row, P, k, sampled, n_out, flags_slice, s_sorted, s_big, s_hash, ctx);
+    const RowIo io_l = {sm.io[0], sm.io[1], sm.io[2], sm.io[3]};
+    finish_row<Elem, PEN, kBlock>(a, row, io_l, P, k, sampled, n_out, flags_slice, s_sorted, s_big, s_hash, ctx);
+    PHASE_MARK(12);
 }
 
 // Merges the S sorted slice lists of each row (one workgroup per row) and
@@ -1162,6 +1397,7 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
     const uint32_t tid = threadIdx.x;
     const uint32_t row = blockIdx.x;
     const nerve_sampler_row_params P = a.params[row];
+    const RowIo io = load_row_io(a, row);
     const bool sampled = P.method != NERVE_METHOD_GREEDY;
     uint32_t k = sampled ? P.top_k : 1u;
     k = k < 1u ? 1u : (k > a.kcap ? a.kcap : k);
@@ -1214,7 +1450,7 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
     ctx.freq = P.frequency_penalty;
     ctx.pres = P.presence_penalty;
     ctx.history = PEN == 2;
-    finish_row<Elem, PEN, kFinishBlock>(a, row, P, k, sampled, n, row_flags, s_sorted, s_big, s_hash, ctx);
+    finish_row<Elem, PEN, kFinishBlock>(a, row, io, P, k, sampled, n, row_flags, s_sorted, s_big, s_hash, ctx);
 }
 
 __global__ void record_tokens_kernel(uint32_t *seen, uint32_t seen_stride, uint32_t rows, const uint32_t *ids,
@@ -1234,10 +1470,6 @@ __global__ void record_tokens_kernel(uint32_t *seen, uint32_t seen_stride, uint3
 
 // ---- launch ------------------------------------------------------------------
 
-template <typename Elem, int EPV>
-static constexpr uint32_t stage_bytes() {
-    return kStageCap * ((uint32_t)sizeof(typename VecTraits<Elem, EPV>::load_t) + 4u);
-}
 
 template <typename Elem, int EPV, int NV, int PEN>
 static hipError_t launch_one(const StepArgs &a0, hipStream_t stream) {
@@ -1341,10 +1573,10 @@ uint32_t stream_lds_bytes(uint32_t variant, bool mask, bool pen, uint32_t hash_s
                           uint32_t kcap) {
     uint32_t stage = 0;
     switch (variant) {
-        case kVariantF32Vec: stage = stage_bytes<float, 4>(); break;
-        case kVariantBf16Vec: stage = stage_bytes<uint16_t, 8>(); break;
-        case kVariantF32Scalar: stage = stage_bytes<float, 1>(); break;
-        default: stage = stage_bytes<uint16_t, 1>(); break;
+        case kVariantF32Vec: stage = stage_area_bytes<float, 4>(); break;
+        case kVariantBf16Vec: stage = stage_area_bytes<uint16_t, 8>(); break;
+        case kVariantF32Scalar: stage = stage_area_bytes<float, 1>(); break;
+        default: stage = stage_area_bytes<uint16_t, 1>(); break;
     }
     return stage + kStreamCandCap * 8u + kcap * 8u + hash_slots * 4u + bitmap_words * 4u * ((pen ? 1u : 0u) + (mask ? 1u : 0u));
 }
