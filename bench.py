@@ -1,24 +1,40 @@
 """Benchmark of the gfx950 sampling stage.
 
 A step is one nerve_sampler_step over one batch of synthetic logits already
-resident in HBM (one fused launch). The default workload is C5, the
-configuration the headline metric is quoted on: B=256 rows x V=151936 bf16
-logits (Student-t(4) * 2), a 2048-id history per row with repetition 1.1 /
-frequency 0.5 / presence 0.3, top-k 50, top-p 0.9, per-row temperature in
-[0.5, 1.2] and a Philox draw. Consecutive steps advance each row's stream
-tick on the device (reference stream-control semantics), so K timed steps are
-K different draws with no host work in between.
+resident in HBM. The default workload is C5, the configuration the headline
+metric is quoted on: B=256 rows x V=151936 bf16 logits (Student-t(4) * 2), a
+2048-id history per row with repetition 1.1 / frequency 0.5 / presence 0.3,
+top-k 50, top-p 0.9, per-row temperature in [0.5, 1.2] and a Philox draw.
+Consecutive steps advance each row's stream tick on the device (reference
+stream-control semantics), so K timed steps are K different draws with no host
+work in between. Steps rotate over --buffers copies of the logits (4 x 78 MB
+by default, more than the 256 MB memory-side cache), so every step reads its
+logits from HBM.
 
 Prints one JSON line: rows/s (whole job), us/step, the HBM roofline of the
-sampling kernel (algorithmic bytes / average kernel time from HIP events on
-the launch stream, against 8 TB/s) and the CPU oracle timed on the host cores
-of the same machine on a bounded sample of the same workload.
+sampling kernel (algorithmic bytes / device time per step from HIP events on
+the launch stream, against 8 TB/s), the HBM traffic per launch measured by
+rocprofv3 counters when a summary of them is present under profiles/, and the
+CPU oracle timed on the host cores of the same machine on a bounded sample of
+the same workload.
+
+Profiling helpers (no JSON line):
+  --calibrate-copy MIB   after the timed steps, run 20 elementwise negations
+                         of MIB MiB each (a kernel that reads and writes a
+                         known number of bytes, to scale the byte counters)
+  --pmc-summary DIR      read the counter_collection.csv files that
+                         `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE`
+                         wrote under DIR and print the per-kernel averages and
+                         the calibrated traffic of the sampling kernel
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
+import re
 import sys
 import time
 
@@ -29,6 +45,8 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 METRIC = "sampled rows/sec + µs/step at B=256×V=151936; % of HBM roofline"
+KERNEL = "sample_rows_kernel"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "sample_rows_kernel_C5_traffic.txt")
 
 
 def parse():
@@ -37,10 +55,13 @@ def parse():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="C5", help="C1..C5 (C5 is the headline workload)")
+    ap.add_argument("--buffers", type=int, default=4, help="logits copies the steps rotate over")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--slices", type=int, default=0, help="workgroups per row (0 = automatic)")
     ap.add_argument("--variant", default="", help="diagnostics: no-history | greedy | no-penalty")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
+    ap.add_argument("--pmc-summary", default="", metavar="DIR")
     return ap.parse_args()
 
 
@@ -73,8 +94,64 @@ def cpu_baseline(w, budget_s: float) -> dict:
     }
 
 
+def read_counters(directory: str) -> dict:
+    """{kernel name: {counter: [per-dispatch values]}} from rocprofv3 CSVs."""
+    out: dict = {}
+    for path in glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                per = out.setdefault(r["Kernel_Name"], {}).setdefault(r["Counter_Name"], {})
+                key = r.get("Dispatch_Id") or r.get("Correlation_Id") or str(len(per))
+                per[key] = per.get(key, 0.0) + float(r["Counter_Value"])
+    return {k: {c: list(v.values()) for c, v in d.items()} for k, d in out.items()}
+
+
+def pmc_summary(directory: str, copy_mib: int) -> None:
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the sampling kernel,
+    scaled by what the same counters read for the known-size negation kernel:
+    factor = known bytes / counted bytes."""
+    counters = read_counters(directory)
+    copy_bytes = copy_mib * 2**20
+    rows = []
+    for name, d in counters.items():
+        for c, v in d.items():
+            rows.append((name, c, float(np.mean(v)), len(v)))
+    for name, c, mean, n in sorted(rows):
+        print(f"{c:10s} {mean:14.1f} KiB  n={n:4d}  {name[:100]}")
+    def pick(pattern, counter):
+        vals = [m for name, c, m, _ in rows if c == counter and re.search(pattern, name)]
+        return max(vals) if vals else None
+    fetch, write = pick(KERNEL, "FETCH_SIZE"), pick(KERNEL, "WRITE_SIZE")
+    cfetch, cwrite = pick("neg_kernel", "FETCH_SIZE"), pick("neg_kernel", "WRITE_SIZE")
+    if fetch is None or cfetch is None:
+        print("missing sampling-kernel or copy-kernel counters")
+        return
+    fr = copy_bytes / (cfetch * 1024.0)
+    wr = copy_bytes / (cwrite * 1024.0) if cwrite else 1.0
+    traffic = fetch * 1024.0 * fr + (write or 0.0) * 1024.0 * wr
+    print(f"calibration kernel: {copy_bytes} B read and written; FETCH_SIZE {cfetch:.1f} KiB -> factor {fr:.4f}; "
+          f"WRITE_SIZE {cwrite} KiB -> factor {wr:.4f}")
+    print(f"traffic_bytes_per_launch = {traffic:.0f}")
+
+
+def measured_traffic(workload: str):
+    """Calibrated HBM bytes per launch from the committed counter summary of
+    this workload, or None."""
+    try:
+        text = open(TRAFFIC_FILE).read()
+    except OSError:
+        return None
+    if f"workload: {workload}" not in text:
+        return None
+    m = re.search(r"traffic_bytes_per_launch = (\d+)", text)
+    return int(m.group(1)) if m else None
+
+
 def main():
     args = parse()
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary, args.calibrate_copy or 256)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(rows are independent: B rows shard over GPUs with no exchange)", file=sys.stderr)
@@ -106,7 +183,9 @@ def main():
         view = {np.uint32: np.int32, np.uint16: np.int16, np.uint64: np.int64}.get(a.dtype.type, a.dtype.type)
         return torch.from_numpy(a.view(view).copy()).to(dev)
 
-    logits = dev_arr(w.logits)
+    nbuf = max(1, args.buffers)
+    logits0 = dev_arr(w.logits)
+    logits = [logits0] + [logits0.clone() for _ in range(nbuf - 1)]
     params = S.params_tensor(w.params, dev)
     history = dev_arr(w.history)
     history_len = dev_arr(w.history_len)
@@ -115,39 +194,41 @@ def main():
     stream_control = torch.zeros((B, 5), dtype=torch.int32, device=dev)
     out = torch.zeros((B, 4), dtype=torch.int32, device=dev)
 
-    def step():
-        sampler.step(logits, params, out, history=history, history_len=history_len, allowed=allowed,
+    def step(i):
+        sampler.step(logits[i % nbuf], params, out, history=history, history_len=history_len, allowed=allowed,
                      seeds=seeds, rng=w.rng, eos_token_id=w.eos_token_id, stream_control=stream_control)
 
-    for _ in range(args.warmup):
-        step()
+    for i in range(args.warmup):
+        step(i)
     torch.cuda.synchronize()
 
-    # whole-step wall clock over K steps
+    # K steps: wall clock on the host, device time from HIP events on the
+    # launch stream (torch's current stream) around the same K launches
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
+    start.record()
+    for i in range(args.steps):
+        step(i)
+    end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-
-    # kernel time from HIP events on the launch stream (torch's current stream)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    for i in range(args.steps):
-        starts[i].record()
-        step()
-        ends[i].record()
-    torch.cuda.synchronize()
-    kern_ms = np.array([s.elapsed_time(e) for s, e in zip(starts, ends)])
-    kern_avg_s = float(np.mean(kern_ms)) / 1e3
+    device_s = start.elapsed_time(end) / 1e3 / args.steps
 
     tick = stream_control[:, 1].cpu().numpy().view(np.uint32)
-    assert (tick == args.warmup + 2 * args.steps).all(), "stream ticks did not advance once per step"
+    assert (tick == args.warmup + args.steps).all(), "stream ticks did not advance once per step"
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy * 2**20 // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            torch.neg(src, out=dst)  # one elementwise kernel: reads and writes exactly MIB MiB
+        torch.cuda.synchronize()
 
     alg_bytes = w.algorithmic_bytes()
-    achieved = alg_bytes / kern_avg_s / 1e9
-    us_per_step = wall / args.steps * 1e6
+    achieved = alg_bytes / device_s / 1e9
+    traffic = measured_traffic(w.name) if not args.variant and args.slices == 0 else None
     res = {
         "metric": METRIC,
         "value": B * args.steps / wall,
@@ -156,11 +237,11 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": wall / args.steps * 1e3,
-        "us_per_step": us_per_step,
+        "us_per_step": wall / args.steps * 1e6,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32" if w.dtype == "f32" else "bf16 logits, f32 arithmetic",
         "data": "synthetic",
         "config": {
             "workload": f"{w.name}: {w.description}",
@@ -170,6 +251,7 @@ def main():
             "top_k": 50 if w.name in ("C3", "C4", "C5") else int(w.params["top_k"][0]),
             "history": 0 if w.history is None else int(w.history.shape[1]),
             "slices_per_row": sampler.slices_per_row,
+            "logits_buffers": nbuf,
             "parallelism": "single GPU; one workgroup per (row, vocab slice)",
         },
         "roofline": {
@@ -178,9 +260,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
-            "kernel": "sample_rows_kernel",
-            "kernel_us": kern_avg_s * 1e6,
+            "traffic": traffic,
+            "kernel": KERNEL,
+            "device_us_per_step": device_s * 1e6,
             "algorithmic_bytes": alg_bytes,
         },
     }

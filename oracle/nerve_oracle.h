@@ -23,7 +23,8 @@
  *                           restatement (nro_sample_row_literal), the reference's
  *                           six sampler tests, closed forms (equal-weight nuclei)
  * Parity with the reference GPU's own exp()/division rounding for non-uniform
- * draws is unpinned: no reference test exercises it.
+ * draws is unpinned: no reference test exercises it, and the reference shaders
+ * cannot run here (no Vulkan); this library defines that rounding.
  */
 #ifndef NERVE_ORACLE_H
 #define NERVE_ORACLE_H
