@@ -1,5 +1,8 @@
 """Builds llmoop_amd/libnerve_sampler.so for gfx950 with hipcc.
 
+Each source compiles to its own object in parallel (the slice kernels are
+split into one translation unit per variant), then hipcc links the library.
+
 Flags that the sampler's bit-exactness depends on:
   -ffp-contract=off                     no fused multiply-add: one rounding per op
   -fno-gpu-flush-denormals-to-zero      binary32 subnormals kept, as on the host
@@ -7,15 +10,17 @@ Flags that the sampler's bit-exactness depends on:
 """
 from __future__ import annotations
 
+import glob
 import os
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libnerve_sampler.so")
-SOURCES = ["nerve_sampler_kernels.hip", "nerve_sampler_api.cpp"]
+OBJDIR = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [
@@ -23,7 +28,6 @@ FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-ffp-contract=off",
     "-fno-gpu-flush-denormals-to-zero",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -33,16 +37,30 @@ FLAGS = [
 ]
 
 
-def build(verbose: bool = False) -> str:
-    cmd = [HIPCC, *FLAGS, "-x", "hip", *[os.path.join(CSRC, s) for s in SOURCES], "-o", LIB]
+def sources() -> list[str]:
+    return sorted(glob.glob(os.path.join(CSRC, "*.hip"))) + [os.path.join(CSRC, "nerve_sampler_api.cpp")]
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("hipcc failed building libnerve_sampler.so")
+        raise RuntimeError(f"hipcc failed: {' '.join(cmd[-3:])}")
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    os.makedirs(OBJDIR, exist_ok=True)
+    srcs = sources()
+    objs = [os.path.join(OBJDIR, os.path.basename(s) + ".o") for s in srcs]
+    cmds = [[HIPCC, *FLAGS, "-x", "hip", "-c", s, "-o", o] for s, o in zip(srcs, objs)]
+    workers = jobs or min(len(cmds), max(1, min(os.cpu_count() or 1, 16)))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        list(pool.map(lambda c: _run(c, verbose), cmds))
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", LIB], verbose)
     return LIB
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose="-v" in sys.argv))

@@ -329,7 +329,7 @@ int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *str
         a.log2_slots = log2u(a.hash_slots);
     }
     const bool pen = b->history != nullptr || b->seen != nullptr;
-    if (pen || b->allowed) a.bitmap_words = nerve::bitmap_words_for(variant, vec_per_slice);
+    if (pen || b->allowed) a.bitmap_words = nerve::bitmap_words_for(variant, nv);
     uint32_t big = nerve::merge_capacity();
     if (slices * d.top_k_capacity > big) big = slices * d.top_k_capacity;
     if (d.top_k_capacity + 32u > big) big = d.top_k_capacity + 32u;  // weights + running sums of the finish step

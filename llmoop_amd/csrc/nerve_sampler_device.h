@@ -1,0 +1,1534 @@
+// nerve_sampler_device.h -- the gfx950 sampling kernels (device code shared by
+// the per-variant translation units that instantiate them).
+//
+// One step samples every row of a decode batch with at most two launches.
+// sample_rows_kernel: each row is split into S vocabulary slices, one 512-lane
+// workgroup per slice (mapped so the slices of a row share one XCD's L2). A
+// workgroup streams its slice from HBM once, in chunks of 8 x 16-byte loads per
+// lane, double-buffered in VGPRs so the loads of chunk c+1 are in flight while
+// chunk c is processed:
+//   - history ids of the slice go into an LDS bitmap and an id -> count hash;
+//     a token with penalty state leaves the stream and re-enters as a patch
+//     entry carrying its configured (masked + penalised) value;
+//   - every other element becomes an order key straight from its raw bits;
+//   - greedy rows keep a per-lane best; sampled rows take a threshold from the
+//     first chunk (the k-th largest per-lane maximum, 16-bit LDS radix select:
+//     at least k keys are >= it) and append every later key >= it to an LDS
+//     candidate list with wave-ballot compaction (about k + a few per chunk
+//     for iid logits). A list that would overflow switches the slice to an
+//     exact radix selection recomputed from memory;
+//   - the candidates are rank-sorted (value desc, id asc) into the slice's
+//     top-k list.
+// With S = 1 the workgroup finishes the row itself; otherwise it writes the
+// list to scratch and finish_rows_kernel (one workgroup per row, same stream,
+// so no cross-workgroup fence) merges the S lists by binary-search ranks, then
+// one wave runs min-p / top-p over the k survivors and the draw.
+//
+// Semantics follow the reference shaders (paths under runtime-rs/shaders/):
+//   greedy_sampler_f32.comp.template:31-34, 52-108       tie-break, argmax, record, tick carry
+//   temperature_top_k_candidates_f32.comp.template:59-126 exact top-k, NaN skipped, -inf never enters
+//   temperature_top_k_top_p_sampler_f32.comp.template:90-216 merge, min-p, top-p, draw, record
+// The greedy path reproduces the reference's NaN behaviour (a lane that starts
+// on a NaN keeps it through the 1024-lane tree) by re-running that exact lane
+// structure for the rare rows that contain a NaN.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <utility>
+
+#include "nerve_device_math.h"
+#include "nerve_sampler_internal.h"
+
+namespace nerve {
+
+#ifdef NERVE_PHASE_TIMING
+// Profiling builds only: per-workgroup shader-clock stamps at phase boundaries.
+__device__ uint64_t g_phase_ts[16384 * 16];
+#define PHASE_MARK(i)                                                                        \
+    do {                                                                                     \
+        if (threadIdx.x == 0 && blockIdx.x < 16384u)                                         \
+            g_phase_ts[blockIdx.x * 16u + (i)] = __builtin_amdgcn_s_memtime();               \
+    } while (0)
+__device__ uint32_t g_dbg[16384 * 4];
+#define DBG_ADD(i, v) atomicAdd(&g_dbg[blockIdx.x * 4u + (i)], (v))
+#define DBG_SET(i, v) (g_dbg[blockIdx.x * 4u + (i)] = (v))
+#else
+#define DBG_ADD(i, v) ((void)0)
+#define DBG_SET(i, v) ((void)0)
+#define PHASE_MARK(i) \
+    do {              \
+    } while (0)
+#endif
+
+constexpr int kBlock = 512;
+constexpr int kWaves = kBlock / 64;
+constexpr int kFinishBlock = 256;
+constexpr uint32_t kCandCap = 1024;
+constexpr uint32_t kHashEmpty = 0xffffffffu;
+constexpr uint32_t kMaxHistory = NERVE_MAX_HISTORY_CAPACITY;
+
+__device__ __forceinline__ uint32_t lane_id() { return __lane_id(); }
+
+// Calls f(std::integral_constant<int, J>) for J = B .. E-1 in order: indices
+// into register arrays stay compile-time however large the body grows.
+template <int B, typename F, int... Js>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, Js...>) {
+    (f(std::integral_constant<int, B + Js>{}), ...);
+}
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (E > B) static_for_impl<B>(f, std::make_integer_sequence<int, E - B>{});
+}
+
+// Workgroup barrier that orders LDS only: waits for this wave's LDS traffic,
+// not for its global loads, so prefetched chunks stay in flight across it.
+__device__ __forceinline__ void lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// The largest t (top B bits significant, the rest zero) with at least `need`
+// of the wave's keys v[] >= t: an MSB-first search with ballot counts. 0 when
+// fewer than `need` keys are nonzero.
+template <int N, int B>
+__device__ __forceinline__ uint32_t wave_kth(const uint32_t (&v)[N], uint32_t need) {
+    uint32_t prefix = 0u;
+#pragma unroll
+    for (int b = 31; b >= 32 - B; --b) {
+        const uint32_t cand = prefix | (1u << b);
+        uint32_t cnt = 0u;
+#pragma unroll
+        for (int i = 0; i < N; ++i) cnt += (uint32_t)__popcll(__ballot(v[i] >= cand));
+        prefix = cnt >= need ? cand : prefix;
+    }
+    return prefix;
+}
+
+__device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
+    const uint32_t lane = lane_id();
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        uint32_t t = __shfl_up(v, o, 64);
+        if (lane >= (uint32_t)o) v += t;
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        uint32_t lo = __shfl_xor((uint32_t)v, o, 64);
+        uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, 64);
+        uint64_t t = ((uint64_t)hi << 32) | lo;
+        v = t > v ? t : v;
+    }
+    return v;
+}
+
+// Exclusive prefix over the block in thread order; `total` gets the block sum.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *s_tmp, uint32_t &total) {
+    const uint32_t tid = threadIdx.x, wave = tid >> 6;
+    uint32_t inc = wave_inclusive_scan(v);
+    if (lane_id() == 63) s_tmp[wave] = inc;
+    lds_sync();
+    uint32_t base = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        uint32_t t = s_tmp[w];
+        base += (uint32_t)w < wave ? t : 0u;
+        tot += t;
+    }
+    lds_sync();
+    total = tot;
+    return base + inc - v;
+}
+
+__device__ __forceinline__ uint32_t block_sum(uint32_t v, uint32_t *s_tmp) {
+    uint32_t total;
+    (void)block_exclusive_scan(v, s_tmp, total);
+    return total;
+}
+
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t *s_tmp) {
+    v = wave_max_u64(v);
+    if (lane_id() == 0) s_tmp[threadIdx.x >> 6] = v;
+    lds_sync();
+    uint64_t m = s_tmp[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) m = s_tmp[w] > m ? s_tmp[w] : m;
+    lds_sync();
+    return m;
+}
+
+// Order key of a binary32 bit pattern (same mapping as order_key()).
+__device__ __forceinline__ uint32_t raw_order_key(uint32_t bits) {
+    const uint32_t mag = bits & 0x7fffffffu;
+    const uint32_t b = mag == 0u ? 0u : bits;
+    const uint32_t key = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return mag > 0x7f800000u ? 0u : key;
+}
+
+__device__ __forceinline__ bool entry_better(uint2 a, uint2 b) {
+    return a.x > b.x || (a.x == b.x && (a.y & kIdMask) < (b.y & kIdMask));
+}
+
+__device__ __forceinline__ float entry_value(uint2 e) {
+    return (e.x == kZeroKey && (e.y & kNegZeroFlag)) ? -0.0f : key_to_float(e.x);
+}
+
+// ---- LDS id -> count table (linear probing, insert-only) ------------------
+
+__device__ __forceinline__ uint32_t hash_slot(uint32_t id, uint32_t log2_slots) {
+    return (id * 0x9E3779B1u) >> (32u - log2_slots);
+}
+
+__device__ __forceinline__ void hash_insert(uint32_t *h, uint32_t log2_slots, uint32_t id) {
+    const uint32_t mask = (1u << log2_slots) - 1u;
+    uint32_t slot = hash_slot(id, log2_slots);
+    for (uint32_t probe = 0; probe <= mask; ++probe) {
+        uint32_t cur = h[slot];
+        if (cur == kHashEmpty) {
+            uint32_t old = atomicCAS(&h[slot], kHashEmpty, (id << 12) | 1u);
+            if (old == kHashEmpty) return;
+            cur = old;
+        }
+        if ((cur >> 12) == id) {
+            atomicAdd(&h[slot], 1u);
+            return;
+        }
+        slot = (slot + 1u) & mask;
+    }
+}
+
+__device__ __forceinline__ uint32_t hash_lookup(const uint32_t *h, uint32_t log2_slots, uint32_t id) {
+    const uint32_t mask = (1u << log2_slots) - 1u;
+    uint32_t slot = hash_slot(id, log2_slots);
+    for (uint32_t probe = 0; probe <= mask; ++probe) {
+        uint32_t cur = h[slot];
+        if (cur == kHashEmpty) return 0u;
+        if ((cur >> 12) == id) return cur & 0xfffu;
+        slot = (slot + 1u) & mask;
+    }
+    return 0u;
+}
+
+// ---- element access ---------------------------------------------------------
+
+template <typename Elem>
+__device__ __forceinline__ float load_elem(const Elem *row, uint32_t t);
+
+template <>
+__device__ __forceinline__ float load_elem<float>(const float *row, uint32_t t) {
+    return row[t];
+}
+
+template <>
+__device__ __forceinline__ float load_elem<uint16_t>(const uint16_t *row, uint32_t t) {
+    return u2f((uint32_t)row[t] << 16);
+}
+
+// One EPV-element slot as loaded from HBM (16 bytes for the vector variants).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename Elem, int EPV>
+struct VecTraits;
+
+// bits(): the binary32 bit pattern of element e (bf16 widens exactly by a shift).
+// upper(): an upper bound of the canonical order keys of the lane-vector's raw
+// values (exact except that -0.0 is lifted to +0.0's key), computed with packed
+// integer ops; has_nan(): whether any raw value is a NaN.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x2 __attribute__((ext_vector_type(2)));
+
+// Order keys of two bf16 values at once: negative -> ~h, else h | 0x8000.
+__device__ __forceinline__ uint32_t bf16x2_keys(uint32_t w) {
+    const i16x2 s = __builtin_bit_cast(i16x2, w) >> (i16x2){15, 15};
+    return w ^ (__builtin_bit_cast(uint32_t, s) | 0x80008000u);
+}
+
+__device__ __forceinline__ uint32_t u16x2_max(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+
+__device__ __forceinline__ uint32_t f32_key_upper(uint32_t w) {
+    const uint32_t key = w ^ ((uint32_t)((int32_t)w >> 31) | 0x80000000u);
+    return key == 0x7fffffffu ? 0x80000000u : key;
+}
+__device__ __forceinline__ uint32_t i32_max(uint32_t a, uint32_t b) { return (uint32_t)max((int32_t)a, (int32_t)b); }
+
+__device__ __forceinline__ uint32_t i16x2_max(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(i16x2, a), __builtin_bit_cast(i16x2, b)));
+}
+
+// Raw-bit maxima. Read as signed integers, the bit patterns of non-negative
+// values order like the values and sit above every negative one, so the
+// signed maximum of a set is its largest value whenever that is >= +0 (and
+// otherwise still one of its elements). vmax() reduces one lane-vector into
+// the accumulator form (packed i16 pairs for bf16, one i32 for f32); merge()
+// folds two accumulators; report_bits() gives the binary32 pattern of report r
+// (0x80000000, the bits of -0.0, is the empty marker); ge_pos(vm, thr) tests
+// whether a vmax() value holds a key >= thr, valid when thr > kZeroKey.
+template <>
+struct VecTraits<float, 4> {
+    using load_t = u32x4;
+    static constexpr int kReports = 1;
+    static constexpr uint32_t kAccInit = 0x80000000u;
+    __device__ static __forceinline__ uint32_t vmax(const load_t &r) { return i32_max(i32_max(r[0], r[1]), i32_max(r[2], r[3])); }
+    __device__ static __forceinline__ uint32_t merge(uint32_t a, uint32_t b) { return i32_max(a, b); }
+    __device__ static __forceinline__ uint32_t report_bits(uint32_t acc, int) { return acc; }
+    __device__ static __forceinline__ bool ge_pos(uint32_t vm, uint32_t thr) { return (int32_t)vm >= (int32_t)(thr & 0x7fffffffu); }
+    __device__ static __forceinline__ uint32_t staged_bits(const load_t *v, uint32_t i, uint32_t e) { return ((const uint32_t *)(v + i))[e]; }
+    __device__ static __forceinline__ uint32_t upper(const load_t &r) {
+        const uint32_t a = max(f32_key_upper(r[0]), f32_key_upper(r[1]));
+        const uint32_t b = max(f32_key_upper(r[2]), f32_key_upper(r[3]));
+        return max(a, b);
+    }
+    __device__ static __forceinline__ bool has_nan(const load_t &r) {
+        const uint32_t m = max(max(r[0] & 0x7fffffffu, r[1] & 0x7fffffffu), max(r[2] & 0x7fffffffu, r[3] & 0x7fffffffu));
+        return m > 0x7f800000u;
+    }
+    __device__ static __forceinline__ uint32_t bits(const load_t &r, int e) { return r[e]; }
+    __device__ static __forceinline__ uint32_t bits_dyn(const load_t &r, uint32_t e) {
+        const uint32_t lo = (e & 1u) ? r[1] : r[0], hi = (e & 1u) ? r[3] : r[2];
+        return (e & 2u) ? hi : lo;
+    }
+};
+
+template <>
+struct VecTraits<uint16_t, 8> {
+    using load_t = u32x4;
+    static constexpr int kReports = 2;
+    static constexpr uint32_t kAccInit = 0x80008000u;
+    __device__ static __forceinline__ uint32_t vmax(const load_t &r) { return i16x2_max(i16x2_max(r[0], r[1]), i16x2_max(r[2], r[3])); }
+    __device__ static __forceinline__ uint32_t merge(uint32_t a, uint32_t b) { return i16x2_max(a, b); }
+    __device__ static __forceinline__ uint32_t report_bits(uint32_t acc, int r) { return r == 0 ? acc << 16 : acc & 0xffff0000u; }
+    __device__ static __forceinline__ bool ge_pos(uint32_t vm, uint32_t thr) {
+        const int32_t m = max((int32_t)(int16_t)(vm & 0xffffu), (int32_t)(int16_t)(vm >> 16));
+        return m >= (int32_t)(((thr & 0x7fffffffu) + 0xffffu) >> 16);
+    }
+    __device__ static __forceinline__ uint32_t staged_bits(const load_t *v, uint32_t i, uint32_t e) {
+        const uint32_t w = ((const uint32_t *)(v + i))[e >> 1];
+        return (e & 1u) ? (w & 0xffff0000u) : (w << 16);
+    }
+    __device__ static __forceinline__ uint32_t upper(const load_t &r) {
+        const uint32_t m2 = u16x2_max(u16x2_max(bf16x2_keys(r[0]), bf16x2_keys(r[1])),
+                                      u16x2_max(bf16x2_keys(r[2]), bf16x2_keys(r[3])));
+        const uint32_t m16 = max(m2 & 0xffffu, m2 >> 16);
+        return m16 == 0x7fffu ? 0x80000000u : ((m16 << 16) | 0xffffu);
+    }
+    __device__ static __forceinline__ bool has_nan(const load_t &r) {
+        const uint32_t t = ((r[0] & 0x7fff7fffu) + 0x007f007fu) | ((r[1] & 0x7fff7fffu) + 0x007f007fu) |
+                           ((r[2] & 0x7fff7fffu) + 0x007f007fu) | ((r[3] & 0x7fff7fffu) + 0x007f007fu);
+        return (t & 0x80008000u) != 0u;
+    }
+    __device__ static __forceinline__ uint32_t bits(const load_t &r, int e) {
+        const uint32_t w = r[e >> 1];
+        return (e & 1) ? (w & 0xffff0000u) : (w << 16);
+    }
+    __device__ static __forceinline__ uint32_t bits_dyn(const load_t &r, uint32_t e) {
+        const uint32_t lo = (e & 2u) ? r[1] : r[0], hi = (e & 2u) ? r[3] : r[2];
+        const uint32_t w = (e & 4u) ? hi : lo;
+        return (e & 1u) ? (w & 0xffff0000u) : (w << 16);
+    }
+};
+
+template <>
+struct VecTraits<float, 1> {
+    using load_t = float;
+    static constexpr int kReports = 1;
+    static constexpr uint32_t kAccInit = 0x80000000u;
+    __device__ static __forceinline__ uint32_t vmax(const load_t &r) { return f2u(r); }
+    __device__ static __forceinline__ uint32_t merge(uint32_t a, uint32_t b) { return i32_max(a, b); }
+    __device__ static __forceinline__ uint32_t report_bits(uint32_t acc, int) { return acc; }
+    __device__ static __forceinline__ bool ge_pos(uint32_t vm, uint32_t thr) { return (int32_t)vm >= (int32_t)(thr & 0x7fffffffu); }
+    __device__ static __forceinline__ uint32_t staged_bits(const load_t *v, uint32_t i, uint32_t) { return f2u(v[i]); }
+    __device__ static __forceinline__ uint32_t upper(const load_t &r) { return f32_key_upper(f2u(r)); }
+    __device__ static __forceinline__ bool has_nan(const load_t &r) { return (f2u(r) & 0x7fffffffu) > 0x7f800000u; }
+    __device__ static __forceinline__ uint32_t bits(const load_t &r, int) { return f2u(r); }
+    __device__ static __forceinline__ uint32_t bits_dyn(const load_t &r, uint32_t) { return f2u(r); }
+};
+
+template <>
+struct VecTraits<uint16_t, 1> {
+    using load_t = uint16_t;
+    static constexpr int kReports = 1;
+    static constexpr uint32_t kAccInit = 0x80000000u;
+    __device__ static __forceinline__ uint32_t vmax(const load_t &r) { return (uint32_t)r << 16; }
+    __device__ static __forceinline__ uint32_t merge(uint32_t a, uint32_t b) { return i32_max(a, b); }
+    __device__ static __forceinline__ uint32_t report_bits(uint32_t acc, int) { return acc; }
+    __device__ static __forceinline__ bool ge_pos(uint32_t vm, uint32_t thr) { return (int32_t)vm >= (int32_t)(thr & 0x7fffffffu); }
+    __device__ static __forceinline__ uint32_t staged_bits(const load_t *v, uint32_t i, uint32_t) { return (uint32_t)v[i] << 16; }
+    __device__ static __forceinline__ uint32_t upper(const load_t &r) { return f32_key_upper((uint32_t)r << 16); }
+    __device__ static __forceinline__ bool has_nan(const load_t &r) { return ((uint32_t)r & 0x7fffu) > 0x7f80u; }
+    __device__ static __forceinline__ uint32_t bits(const load_t &r, int) { return (uint32_t)r << 16; }
+    __device__ static __forceinline__ uint32_t bits_dyn(const load_t &r, uint32_t) { return (uint32_t)r << 16; }
+};
+
+// Row state shared by the helpers that recompute a single configured value.
+struct RowCtx {
+    const void *logits_row;
+    const uint32_t *allowed_row;
+    const uint32_t *seen_row;
+    const uint32_t *hash;      // LDS
+    // LDS bitmap of the slice's history ids (from tok0) with `hash` holding
+    // the occurrences beyond the first; or null, and `hash` holds full counts
+    const uint32_t *bitmap;
+    uint32_t log2_slots;
+    uint32_t tok0;
+    float rep, freq, pres;
+    bool history;
+};
+
+template <typename Elem>
+__device__ __forceinline__ float configured_at(const RowCtx &c, uint32_t t) {
+    float x = load_elem<Elem>((const Elem *)c.logits_row, t);
+    bool allowed = c.allowed_row ? ((c.allowed_row[t >> 5] >> (t & 31u)) & 1u) : true;
+    uint32_t count = 0;
+    if (c.history) {
+        if (c.bitmap) {
+            const uint32_t o = t - c.tok0;
+            if ((c.bitmap[o >> 5] >> (o & 31u)) & 1u) count = 1u + hash_lookup(c.hash, c.log2_slots, t);
+        } else {
+            count = hash_lookup(c.hash, c.log2_slots, t);
+        }
+    } else if (c.seen_row) {
+        count = (c.seen_row[t >> 5] >> (t & 31u)) & 1u;
+    }
+    return configured_logit(x, allowed, count, c.rep, c.freq, c.pres);
+}
+
+__device__ __forceinline__ bool float_better(float cl, uint32_t cid, float bl, uint32_t bid) {
+    return cl > bl || (cl == bl && cid < bid);
+}
+
+// ---- radix select over per-lane key arrays --------------------------------
+//
+// Returns a key threshold t: the first `passes` bytes of the k-th largest
+// nonzero key (lower bytes zero), so #{key >= t} >= k. Returns 1 ("every
+// nonzero key") when fewer than k keys are nonzero. `count_ge` receives the
+// number of keys >= t when passes == 4 or the fewer-than-k case applies.
+template <int N>
+__device__ __forceinline__ uint32_t radix_threshold(const uint32_t (&v)[N], uint32_t k, int passes, uint32_t *s_hist,
+                                    uint32_t *s_sel, uint32_t &count_ge) {
+    const uint32_t tid = threadIdx.x;
+    uint32_t prefix = 0, remaining = k, above_total = 0;
+    count_ge = 0;
+    for (int p = 0; p < passes; ++p) {
+        const int shift = 24 - 8 * p;
+        const uint32_t hmask = p == 0 ? 0u : (0xffffffffu << (shift + 8));
+        for (uint32_t i = tid; i < 256u; i += kBlock) s_hist[i] = 0u;
+        lds_sync();
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            uint32_t x = v[i];
+            if (x != 0u && (x & hmask) == prefix) atomicAdd(&s_hist[(x >> shift) & 255u], 1u);
+        }
+        lds_sync();
+        if (tid < 64) {
+            const uint32_t lane = tid;
+            uint32_t c[4], sum = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                c[q] = s_hist[255u - 4u * lane - (uint32_t)q];
+                sum += c[q];
+            }
+            uint32_t incl = wave_inclusive_scan(sum);
+            uint32_t excl = incl - sum;
+            if (excl < remaining && remaining <= incl) {
+                uint32_t acc = excl;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if (acc < remaining && acc + c[q] >= remaining) {
+                        s_sel[0] = 255u - 4u * lane - (uint32_t)q;
+                        s_sel[1] = acc;
+                        s_sel[2] = c[q];
+                    }
+                    acc += c[q];
+                }
+            }
+            if (lane == 63 && incl < remaining) {
+                s_sel[0] = 0xffffffffu;
+                s_sel[1] = incl;
+            }
+        }
+        lds_sync();
+        const uint32_t d = s_sel[0], above = s_sel[1], in_bin = s_sel[2];
+        lds_sync();
+        if (d == 0xffffffffu) {
+            count_ge = above_total + above;
+            return 1u;
+        }
+        remaining -= above;
+        above_total += above;
+        prefix |= d << shift;
+        count_ge = above_total + in_bin;
+    }
+    return prefix;
+}
+
+// Same contract as radix_threshold (all four bytes), over the tokens
+// [t0, t1) of a slice with keys produced by `key_of(t)`; used by the rare
+// exact path, which recomputes keys from memory instead of holding them.
+template <typename KeyFn>
+__device__ __forceinline__ uint32_t radix_threshold_fn(uint32_t t0, uint32_t t1, uint32_t k, uint32_t *s_hist, uint32_t *s_sel,
+                                       uint32_t &count_ge, KeyFn key_of) {
+    const uint32_t tid = threadIdx.x;
+    uint32_t prefix = 0, remaining = k, above_total = 0;
+    count_ge = 0;
+    for (int p = 0; p < 4; ++p) {
+        const int shift = 24 - 8 * p;
+        const uint32_t hmask = p == 0 ? 0u : (0xffffffffu << (shift + 8));
+        for (uint32_t i = tid; i < 256u; i += kBlock) s_hist[i] = 0u;
+        lds_sync();
+        for (uint32_t t = t0 + tid; t < t1; t += kBlock) {
+            const uint32_t x = key_of(t);
+            if (x != 0u && (x & hmask) == prefix) atomicAdd(&s_hist[(x >> shift) & 255u], 1u);
+        }
+        lds_sync();
+        if (tid < 64) {
+            const uint32_t lane = tid;
+            uint32_t c[4], sum = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                c[q] = s_hist[255u - 4u * lane - (uint32_t)q];
+                sum += c[q];
+            }
+            const uint32_t incl = wave_inclusive_scan(sum);
+            const uint32_t excl = incl - sum;
+            if (excl < remaining && remaining <= incl) {
+                uint32_t acc = excl;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if (acc < remaining && acc + c[q] >= remaining) {
+                        s_sel[0] = 255u - 4u * lane - (uint32_t)q;
+                        s_sel[1] = acc;
+                        s_sel[2] = c[q];
+                    }
+                    acc += c[q];
+                }
+            }
+            if (lane == 63 && incl < remaining) {
+                s_sel[0] = 0xffffffffu;
+                s_sel[1] = incl;
+            }
+        }
+        lds_sync();
+        const uint32_t d = s_sel[0], above = s_sel[1], in_bin = s_sel[2];
+        lds_sync();
+        if (d == 0xffffffffu) {
+            count_ge = above_total + above;
+            return 1u;
+        }
+        remaining -= above;
+        above_total += above;
+        prefix |= d << shift;
+        count_ge = above_total + in_bin;
+    }
+    return prefix;
+}
+
+// ---- the fused kernel -------------------------------------------------------
+
+struct SharedSmall {
+    uint32_t hist[256];
+    uint32_t sel[4];
+    uint32_t scan[kWaves];
+    uint64_t red[kWaves];
+    uint32_t flag[4];
+    uint32_t ones[1];  // all-ones mask word of rows without a mask
+    uint32_t io[4];                  // the row's RowIo, stored during the set-up
+    uint32_t ukeys[2][kWaves * 64];  // report unions of the two threshold passes
+    uint32_t ucount[2][kWaves];
+};
+
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t n) {
+    // Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
+    // contiguous run of logical ids so the slices of a row share one L2.
+    const uint32_t q = n / 8u, rem = n % 8u;
+    const uint32_t xcd = b % 8u, idx = b / 8u;
+    return xcd < rem ? xcd * (q + 1u) + idx : rem * (q + 1u) + (xcd - rem) * q + idx;
+}
+
+// Per-row draw inputs, read at kernel start so their latency hides behind
+// the stream: the seed, the tick (stream control words 1-2, else the step),
+// and the output ring capacity (stream control word 4).
+struct RowIo {
+    uint32_t seed, tick_lo, tick_hi, ring_cap;
+};
+
+__device__ __forceinline__ RowIo load_row_io(const StepArgs &a, uint32_t row) {
+    RowIo io;
+    io.seed = a.seeds ? a.seeds[row] : 0u;
+    if (a.stream_control) {
+        const uint32_t *sc = a.stream_control + (uint64_t)row * 5u;
+        io.tick_lo = sc[1];
+        io.tick_hi = sc[2];
+        io.ring_cap = sc[4];
+    } else {
+        const uint64_t t = a.steps ? a.steps[row] : 0ull;
+        io.tick_lo = (uint32_t)t;
+        io.tick_hi = (uint32_t)(t >> 32);
+        io.ring_cap = 0u;
+    }
+    return io;
+}
+
+// Finishes one row from its sorted survivors s_sorted[0 .. n) (value desc,
+// id asc): EOS fallback for an all-zero mask, the greedy record (replaying the
+// reference's 1024-lane argmax when the row holds a NaN), or min-p / top-p over
+// the k survivors and the draw (temperature_top_k_top_p_sampler_f32:157-216).
+// Writes the output record, optional survivors / probabilities, the stream
+// control tick and the output ring. Runs on NT threads; wave 0 does the
+// sequential running sums.
+template <typename Elem, int PEN, int NT>
+__device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, const RowIo &io, const nerve_sampler_row_params &P, uint32_t k,
+                           bool sampled, uint32_t n, uint32_t row_flags, uint2 *s_sorted, uint2 *s_big,
+                           uint32_t *s_hash, const RowCtx &ctx) {
+    __shared__ uint32_t s_res[2];
+    const uint32_t tid = threadIdx.x;
+    float *s_w = (float *)s_big;                 // [kcap + 64] weights, zero past the min-p cut
+    float *s_p = (float *)s_big + a.kcap + 64u;  // [kcap] running sums, then probabilities
+    uint32_t token = 0, sel_bits = 0, out_flags = 0, kout = 1;
+    uint32_t *sc = a.stream_control ? a.stream_control + (uint64_t)row * 5u : nullptr;
+
+    const bool eos = a.allowed && !(row_flags & 1u);
+    if (eos) {
+        token = a.eos;
+        sel_bits = 0xff800000u;  // -inf: every token was masked
+        out_flags = NERVE_FLAG_EOS_FALLBACK | (sampled ? NERVE_FLAG_SAMPLED : 0u);
+        if (tid == 0) s_p[0] = 1.0f;
+    } else if (!sampled) {
+        if (row_flags & 2u) {
+            // A NaN in the row: replay the reference lane structure exactly
+            // (greedy_sampler_f32:52-83), with penalties for the whole row.
+            if constexpr (PEN == 2) {
+                for (uint32_t i = tid; i < a.hash_slots; i += NT) s_hash[i] = kHashEmpty;
+                __syncthreads();
+                uint32_t len = a.history_len[row];
+                len = len > a.history_stride ? a.history_stride : len;
+                const uint32_t *hrow = a.history + (uint64_t)row * a.history_stride;
+                for (uint32_t i = tid; i < len; i += NT)
+                    if (hrow[i] < a.vocab) hash_insert(s_hash, a.log2_slots, hrow[i]);
+            }
+            __syncthreads();
+            RowCtx full = ctx;
+            full.bitmap = nullptr;
+            uint2 *slots = s_big;  // 1024 entries of (float bits, id)
+            for (uint32_t L = tid; L < 1024u; L += NT) {
+                uint32_t bid = L;
+                float best = L < a.vocab ? configured_at<Elem>(full, L) : u2f(kLowestBits);
+                for (uint32_t t = L + 1024u; t < a.vocab; t += 1024u) {
+                    const float c = configured_at<Elem>(full, t);
+                    if (float_better(c, t, best, bid)) {
+                        best = c;
+                        bid = t;
+                    }
+                }
+                slots[L] = make_uint2(f2u(best), bid);
+            }
+            __syncthreads();
+            for (uint32_t stride = 512u; stride > 0u; stride >>= 1) {
+                for (uint32_t L = tid; L < stride; L += NT) {
+                    const uint2 c = slots[L + stride], b = slots[L];
+                    if (float_better(u2f(c.x), c.y, u2f(b.x), b.y)) slots[L] = c;
+                }
+                __syncthreads();
+            }
+            token = slots[0].y;
+            sel_bits = slots[0].x;
+        } else {
+            const uint2 e = s_sorted[0];
+            if (e.x == kNegInfKey && a.vocab < 1024u) {
+                // every token is -inf: the shader's padded lane V (LOWEST_FLOAT) wins
+                token = a.vocab;
+                sel_bits = kLowestBits;
+            } else {
+                token = e.y & kIdMask;
+                sel_bits = f2u(entry_value(e));
+            }
+        }
+        __syncthreads();
+        if (tid == 0) s_p[0] = 1.0f;
+    } else {
+        for (uint32_t i = n + tid; i < k; i += NT) s_sorted[i] = make_uint2(kMinFiniteKey, kPadId);
+        __syncthreads();
+        if (tid < 64) {
+            const uint32_t lane = tid;
+            const float T = P.temperature;
+            // the uniform draw does not depend on the weights: start it first
+            const uint64_t tick = (uint64_t)io.tick_lo | ((uint64_t)io.tick_hi << 32);
+            const float u = random_unit(a.rng, io.seed, tick, row);
+            const float l0 = entry_value(s_sorted[0]);
+            const float m = l0 / T;
+            float minimum = u2f(kLowestBits);
+            if (P.min_p > 0.0f) {
+                const float lg = nerve_logf(P.min_p);
+                const float d = T * lg;
+                minimum = l0 + d;
+            }
+            PHASE_MARK(13);
+            // Per chunk of 64 survivors: the min-p cut (the first survivor
+            // below the floor ends the list), the weights, and the running
+            // sums in the reference's sequential order: lane i adds w_c0,
+            // w_c0+1, ... in turn and +0.0 (exact) for the terms after its own,
+            // so its sum is the reference's prefix sum P_i, rounding for
+            // rounding. s_w is zero past the cut.
+            uint32_t n_valid = k;
+            float carry = 0.0f;  // P_(c0 - 1)
+            for (uint32_t c0 = 0; c0 < n_valid; c0 += 64u) {
+                const uint32_t i = c0 + lane;
+                const float v = i < k ? entry_value(s_sorted[i]) : 0.0f;
+                const uint64_t below = __ballot(i < k && v < minimum);
+                if (below) n_valid = min(n_valid, c0 + (uint32_t)__builtin_ctzll(below));
+                if (c0 >= n_valid) break;
+                const bool in = i < n_valid;
+                s_w[i] = in ? nerve_expf(v / T - m) : 0.0f;
+                PHASE_MARK(14);
+                float wv[64];
+                static_for<0, 64>([&](auto J) __attribute__((always_inline)) { wv[J] = s_w[c0 + (uint32_t)J]; });
+                float acc = carry;
+                static_for<0, 64>([&](auto J) __attribute__((always_inline)) {
+                    acc = acc + ((uint32_t)J <= lane ? wv[J] : 0.0f);
+                });
+                s_p[i] = acc;
+                carry = u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(min(64u, n_valid - c0) - 1u)));
+            }
+            PHASE_MARK(10);
+            const float total = n_valid ? carry : 0.0f;
+            const float threshold = P.top_p * total;
+            uint32_t nucleus = n_valid;
+            for (uint32_t c0 = 0; c0 < n_valid; c0 += 64u) {
+                const uint32_t i = c0 + lane;
+                const uint64_t b = __ballot(i < n_valid && s_p[i] >= threshold);
+                if (b) {
+                    nucleus = c0 + (uint32_t)__builtin_ctzll(b) + 1u;
+                    break;
+                }
+            }
+            if (nucleus == 0u) nucleus = 1u;
+            const float nucleus_weight = n_valid ? s_p[nucleus - 1u] : 0.0f;
+            PHASE_MARK(15);
+            const float target = u * nucleus_weight;
+            uint32_t selected = nucleus - 1u;
+            for (uint32_t c0 = 0; c0 < nucleus && c0 < n_valid; c0 += 64u) {
+                const uint32_t i = c0 + lane;
+                const uint64_t b = __ballot(i < nucleus && i < n_valid && target < s_p[i]);
+                if (b) {
+                    selected = c0 + (uint32_t)__builtin_ctzll(b);
+                    break;
+                }
+            }
+            for (uint32_t i = lane; i < k; i += 64u) s_p[i] = (i < nucleus && i < n_valid) ? s_w[i] / nucleus_weight : 0.0f;
+            if (lane == 0) {
+                const uint2 e = s_sorted[selected];
+                s_res[0] = e.y == kPadId ? kPadId : (e.y & kIdMask);
+                s_res[1] = f2u(entry_value(e));
+            }
+        }
+        __syncthreads();
+        PHASE_MARK(11);
+        token = s_res[0];
+        sel_bits = s_res[1];
+        out_flags = NERVE_FLAG_SAMPLED;
+        kout = k;
+    }
+    __syncthreads();
+
+    if (tid == 0) {
+        nerve_sampler_output o;
+        o.token_id = token;
+        o.selected_logit_bits = sel_bits;
+        o.flags = out_flags;
+        o.reserved = 0u;
+        a.out[row] = o;
+        if (sc) {
+            const uint32_t lo = io.tick_lo;
+            if (a.ring) {
+                uint32_t *ring = a.ring + (uint64_t)row * a.ring_stride;
+                const uint32_t cap = io.ring_cap;
+                ring[0] = token; ring[1] = sel_bits; ring[2] = out_flags; ring[3] = 0u;
+                if (cap) {
+                    const uint64_t w = 4ull + (uint64_t)(lo % cap) * 4ull;
+                    if (w + 4ull <= a.ring_stride) {
+                        ring[w] = token; ring[w + 1] = sel_bits; ring[w + 2] = out_flags; ring[w + 3] = 0u;
+                    }
+                }
+            }
+            sc[0] = token;
+            const uint32_t next = lo + 1u;
+            if (next == 0u) sc[2] = io.tick_hi + 1u;
+            sc[1] = next;
+        }
+    }
+    if (a.topk_ids || a.topk_logits || a.topk_probs) {
+        for (uint32_t i = tid; i < a.kcap; i += NT) {
+            const uint64_t o = (uint64_t)row * a.kcap + i;
+            const bool live = i < kout;
+            float value = u2f(kLowestBits);
+            uint32_t id = kPadId;
+            if (live && i == 0 && (eos || !sampled)) {
+                value = eos ? u2f(kLowestBits) : u2f(sel_bits);
+                id = token;
+            } else if (live) {
+                const uint2 e = s_sorted[i];
+                value = entry_value(e);
+                id = e.y == kPadId ? kPadId : (e.y & kIdMask);
+            }
+            if (a.topk_ids) a.topk_ids[o] = id;
+            if (a.topk_logits) a.topk_logits[o] = value;
+            if (a.topk_probs) a.topk_probs[o] = live ? s_p[i] : 0.0f;
+        }
+    }
+}
+
+constexpr uint32_t kStageCap = 1024;       // lane-vectors staged for exact work per slice
+constexpr uint32_t kStreamCandCap = 2048;  // candidate entries per slice
+
+// Bytes of the staging area (lane-vectors and their slots).
+template <typename Elem, int EPV>
+__host__ __device__ constexpr uint32_t stage_area_bytes() {
+    return kStageCap * ((uint32_t)sizeof(typename VecTraits<Elem, EPV>::load_t) + 4u);
+}
+
+// Bitmap words of a slice: its tokens [tok0, tok1) rounded out to 32-token
+// words, plus slack; the host sizes the LDS bitmaps with the same bound.
+__host__ __device__ constexpr uint32_t slice_bitmap_words(uint32_t tokens, uint32_t epv) {
+    return (tokens + epv + 62u) / 32u + 1u;
+}
+
+// PEN: 0 = no penalty state, 1 = seen bitmap (set semantics), 2 = history ids
+// (count semantics). EPV elements per lane-vector, NV lane-vectors per lane.
+//
+// The slice [v0, v1) of full lane-vectors lives in VGPRs: wave w owns slots
+// v0 + w * 64 * NV + [0, 64 * NV), and lane-vector j of lane l is the slot
+// 64 * j + l of that run. Every load is issued before any selection work, then
+//   pass 1  as the loads land, two signed-integer maxima per lane over the
+//           lane-vectors with no penalty state and no masked element; every
+//           report is a real element, so the k-th largest report key is a
+//           lower bound of the slice's k-th largest configured key;
+//   select  that k-th largest report (LDS radix select) -> thr;
+//   pass 2  lane-vectors whose raw maximum reaches thr are staged in LDS;
+//   exact   one lane per staged lane-vector computes configured keys and
+//           appends keys >= thr to the candidate list.
+// Penalties that never raise a logit (repetition >= 1, frequency and presence
+// >= 0) keep configured <= raw, so the raw test is conservative for penalised
+// tokens too. Other settings take penalised tokens out of the vector passes
+// and evaluate each one from the history table instead (one gather per id).
+template <typename Elem, int EPV, int NV, int PEN, bool MASK>
+__global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
+    constexpr int HPT = (kMaxHistory + kBlock - 1) / kBlock;  // history ids per lane
+    constexpr int BW = (int)((slice_bitmap_words((uint32_t)kBlock * NV * EPV, EPV) + kBlock - 1u) / kBlock);
+    constexpr int LW = (NV + 31) / 32;
+    constexpr uint32_t kFull = EPV == 32 ? 0xffffffffu : ((1u << EPV) - 1u);
+    constexpr bool history = PEN == 2;
+    using VT = VecTraits<Elem, EPV>;
+    using vec_t = typename VT::load_t;
+    constexpr uint32_t kVecBytes = (uint32_t)sizeof(vec_t);
+    __shared__ SharedSmall sm;
+    extern __shared__ __align__(16) uint32_t s_dyn[];
+    uint32_t *s_hash = s_dyn;                                      // [hash_slots], a multiple of 64
+    vec_t *s_svec = (vec_t *)(s_hash + a.hash_slots);              // [kStageCap]
+    uint32_t *s_sslot = (uint32_t *)(s_svec + kStageCap);          // [kStageCap]
+    uint2 *s_cand = (uint2 *)(s_sslot + kStageCap);                // [kStreamCandCap], later finish scratch
+    uint2 *s_sorted = s_cand + kStreamCandCap;                     // [kcap]
+    uint32_t *s_pen = (uint32_t *)(s_sorted + a.kcap);             // [bitmap_words] when PEN != 0
+    uint32_t *s_allow = s_pen + (PEN != 0 ? a.bitmap_words : 0u);  // [bitmap_words] with a mask
+    uint2 *s_big = s_cand;
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t logical = xcd_remap(blockIdx.x, gridDim.x);
+    const uint32_t row = logical / a.slices;
+    const uint32_t slice = logical % a.slices;
+
+    const nerve_sampler_row_params P = a.params[row];
+    const RowIo io = a.slices == 1u ? load_row_io(a, row) : RowIo{0u, 0u, 0u, 0u};
+    const bool sampled = P.method != NERVE_METHOD_GREEDY;
+    uint32_t k = sampled ? P.top_k : 1u;
+    k = k < 1u ? 1u : (k > a.kcap ? a.kcap : k);
+    const uint32_t valid_min = sampled ? kMinFiniteKey : kNegInfKey;
+    const uint32_t masked_key = sampled ? 0u : kNegInfKey;
+    constexpr bool mask = MASK;  // an allowed-token bitmask is present
+    const bool lowering = P.repetition_penalty >= 1.0f && P.frequency_penalty >= 0.0f && P.presence_penalty >= 0.0f;
+
+    const uint32_t nfull = a.nvec;
+    const uint32_t v0 = min(slice * a.vec_per_slice, nfull);
+    const uint32_t v1 = min(v0 + a.vec_per_slice, nfull);
+    const bool last_slice = slice == a.slices - 1u;
+    const uint32_t tok0 = v0 * EPV;
+    const uint32_t tok1 = last_slice ? a.vocab : v1 * EPV;
+    const uint32_t bm_base = tok0 & ~31u;
+    const uint32_t bm_n = tok1 > tok0 ? ((tok1 - 1u) >> 5) - (bm_base >> 5) + 1u : 0u;
+    const uint32_t tail_id = nfull * EPV + tid;
+    const bool has_tail = last_slice && tail_id < a.vocab;
+
+    const Elem *lrow = (const Elem *)a.logits + (uint64_t)row * a.ld;
+    const uint32_t *arow = mask ? a.allowed + (uint64_t)row * a.allowed_stride : nullptr;
+    const uint32_t *srow = PEN == 1 ? a.seen + (uint64_t)row * a.seen_stride : nullptr;
+
+    PHASE_MARK(0);
+    // 1. loads: history ids and bitmap words first (they are needed first),
+    // then the first D lane-vectors through a buffer resource bounded by v1
+    // (a slot past the slice reads as zero and is never used). A wave owns
+    // 64 * NV consecutive slots, so the loads of a lane sit 64 slots apart and
+    // share one offset register per 4 KiB.
+    const uint32_t lane = lane_id();
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // the slice is spread evenly: wave w owns `span` slots from w * span
+    const uint32_t span = ((a.vec_per_slice + (uint32_t)kBlock - 1u) / (uint32_t)kBlock) * 64u;
+    const uint32_t wslots = v1 - v0 > wave * span ? min(span, v1 - v0 - wave * span) : 0u;  // valid slots of the wave
+    const uint32_t wbase = wave * span + lane;  // slot of lane-vector 0, relative to v0
+    uint32_t hist[history ? HPT : 1];
+    uint32_t hlen = 0;
+    if constexpr (history) {
+        const uint32_t *hrow = a.history + (uint64_t)row * a.history_stride;
+        const uint32_t hlast = a.history_stride - 1u;
+#pragma unroll
+        for (int h = 0; h < HPT; ++h) hist[h] = hrow[min(tid + (uint32_t)h * kBlock, hlast)];
+        hlen = min(a.history_len[row], a.history_stride);
+    }
+    const uint32_t bm_last = bm_n ? bm_n - 1u : 0u;
+    uint32_t mw[BW];
+    if (mask) {
+#pragma unroll
+        for (int i = 0; i < BW; ++i) mw[i] = arow[(bm_base >> 5) + min(tid + (uint32_t)i * kBlock, bm_last)];
+    }
+    uint32_t sw[PEN == 1 ? BW : 1];
+    if constexpr (PEN == 1) {
+#pragma unroll
+        for (int i = 0; i < BW; ++i) sw[i] = srow[(bm_base >> 5) + min(tid + (uint32_t)i * kBlock, bm_last)];
+    }
+    // per-wave buffer resource: a load past the wave's valid run reads zero
+    // and costs no memory traffic
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(lrow + (uint64_t)(v0 + wave * span) * EPV), (short)0, (int)(wslots * kVecBytes), 0x00020000);
+    vec_t data[NV];
+    auto load = [&](int j) __attribute__((always_inline)) {
+        const uint32_t off = (lane + (uint32_t)j * 64u) * kVecBytes;
+        if constexpr (kVecBytes == 16) data[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
+        else if constexpr (kVecBytes == 4) data[j] = u2f(__builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, 0));
+        else data[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
+    };
+    // lane-vectors in flight ahead of the one being processed
+#ifndef NERVE_LOOKAHEAD
+#define NERVE_LOOKAHEAD 16
+#endif
+    constexpr int D = NV < NERVE_LOOKAHEAD ? NV : NERVE_LOOKAHEAD;
+    static_for<0, D>([&](auto J) __attribute__((always_inline)) { load(J); });
+    PHASE_MARK(1);
+
+    // 2. LDS state: counters, mask / seen words of the slice (bits outside
+    // [tok0, tok1) cleared); history ids -> bitmap, and repeats -> a table of
+    // occurrences beyond the first
+    if constexpr (history) {
+        const uint4 empty4 = make_uint4(kHashEmpty, kHashEmpty, kHashEmpty, kHashEmpty);
+        for (uint32_t i = tid; i < a.hash_slots / 4u; i += kBlock) ((uint4 *)s_hash)[i] = empty4;
+        for (uint32_t i = tid; i < bm_n; i += kBlock) s_pen[i] = 0u;
+    }
+    if (tid == 0) {
+        sm.flag[1] = 0u;  // candidates
+        sm.flag[2] = 0u;  // staged lane-vectors
+        sm.flag[3] = 0u;  // slice flags
+        sm.ones[0] = 0xffffffffu;
+        sm.io[0] = io.seed;
+        sm.io[1] = io.tick_lo;
+        sm.io[2] = io.tick_hi;
+        sm.io[3] = io.ring_cap;
+    }
+    auto range_bits = [&](uint32_t w) __attribute__((always_inline)) -> uint32_t {
+        const uint32_t t = bm_base + w * 32u;
+        uint32_t m = 0xffffffffu;
+        if (t < tok0) m &= 0xffffffffu << (tok0 - t);
+        if (t + 32u > tok1) m &= (tok1 - t) >= 32u ? 0xffffffffu : ((1u << (tok1 - t)) - 1u);
+        return m;
+    };
+    uint32_t any_allowed = mask ? 0u : (tok1 > tok0 ? 1u : 0u);
+    if (mask) {
+#pragma unroll
+        for (int i = 0; i < BW; ++i) {
+            const uint32_t w = tid + (uint32_t)i * kBlock;
+            if (w < bm_n) {
+                const uint32_t v = mw[i] & range_bits(w);
+                s_allow[w] = v;
+                any_allowed |= v ? 1u : 0u;
+            }
+        }
+    }
+    if constexpr (PEN == 1) {
+#pragma unroll
+        for (int i = 0; i < BW; ++i) {
+            const uint32_t w = tid + (uint32_t)i * kBlock;
+            if (w < bm_n) s_pen[w] = sw[i] & range_bits(w);
+        }
+    }
+    lds_sync();
+    if constexpr (history) {
+        uint32_t first[HPT];
+#pragma unroll
+        for (int h = 0; h < HPT; ++h) {
+            const uint32_t id = hist[h];
+            first[h] = 0xffffffffu;
+            if (tid + (uint32_t)h * kBlock < hlen && id >= tok0 && id < tok1) {
+                const uint32_t o = id - bm_base;
+                first[h] = atomicOr(&s_pen[o >> 5], 1u << (o & 31u)) & (1u << (o & 31u));
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < HPT; ++h)
+            if (first[h] != 0xffffffffu && first[h] != 0u) hash_insert(s_hash, a.log2_slots, hist[h]);
+        lds_sync();
+    }
+    PHASE_MARK(2);
+
+    // 3. the stream. Lane-vector j is processed as it lands while lane-vector
+    // j + D is issued. Per group of 8: the flags from the LDS bitmaps (ok =
+    // every element valid, allowed and free of penalty state; live = some
+    // element valid and allowed). Pass 1 folds ok lane-vectors into the lane
+    // reports. After the first half, thr (a lower bound of the slice's k-th
+    // largest key, from the reports so far) is set and pass 2 stages every
+    // lane-vector that can hold a key >= thr, first-half ones included.
+    const uint32_t nval = wslots > lane ? (wslots - lane + 63u) / 64u : 0u;  // valid lane-vectors of this lane
+    uint32_t okm[LW], live[LW], vmask[LW];
+#pragma unroll
+    for (int i = 0; i < LW; ++i) {
+        const uint32_t lo = (uint32_t)i * 32u;
+        const uint32_t n = nval > lo ? min(nval - lo, 32u) : 0u;
+        vmask[i] = n >= 32u ? 0xffffffffu : ((1u << n) - 1u);  // valid lane-vectors
+        okm[i] = vmask[i];
+        live[i] = vmask[i];
+    }
+    // Lane-vector j of this lane starts at bitmap bit tok_base + 64 * EPV * j:
+    // the word moves by a constant (an immediate offset) and the bit position
+    // stays put. The bitmaps are sized for NV full lane-vectors per lane, so
+    // the reads of invalid ones stay inside them (their flags are masked).
+    const uint32_t tok_base = (v0 + wbase) * EPV - bm_base;
+    const uint32_t wsh = tok_base & 31u;
+    const uint32_t *pen_w = s_pen + (tok_base >> 5);
+    const uint32_t *allow_w = s_allow + (tok_base >> 5);
+    constexpr uint32_t kWordsPerJ = 64u * EPV / 32u;
+    auto flags_group = [&](auto mask_tag, auto J0) __attribute__((always_inline)) {
+        constexpr bool M = decltype(mask_tag)::value;
+        constexpr int j0 = decltype(J0)::value;
+        uint32_t aw[8], pw[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            if constexpr (M) aw[q] = allow_w[(uint32_t)(j0 + q) * kWordsPerJ];
+            if constexpr (PEN != 0) pw[q] = pen_w[(uint32_t)(j0 + q) * kWordsPerJ];
+        }
+        uint32_t okg = 0u, lvg = 0u;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            bool ok = true, lv = true;
+            if constexpr (M) {
+                const uint32_t ab = (aw[q] >> wsh) & kFull;
+                ok = ab == kFull;
+                lv = ab != 0u;
+            }
+            if constexpr (PEN != 0) ok = ok && ((pw[q] >> wsh) & kFull) == 0u;
+            okg |= ok ? (1u << q) : 0u;
+            lvg |= lv ? (1u << q) : 0u;
+        }
+        const int sh = j0 & 31;
+        okm[j0 >> 5] &= ~(0xffu << sh) | (okg << sh);
+        live[j0 >> 5] &= ~(0xffu << sh) | (lvg << sh);
+    };
+    auto flags_at = [&](auto J0) __attribute__((always_inline)) {
+        if constexpr (MASK || PEN != 0) flags_group(std::integral_constant<bool, MASK>{}, J0);
+    };
+    uint32_t acc0 = VT::kAccInit, acc1 = VT::kAccInit;
+    auto pass1 = [&](int j) __attribute__((always_inline)) {
+        // branch-free: a lane-vector that is not ok contributes the empty marker
+        const uint32_t sel = 0u - ((okm[j >> 5] >> (j & 31)) & 1u);
+        const uint32_t vm = (VT::vmax(data[j]) & sel) | (VT::kAccInit & ~sel);
+        if (j & 1) acc1 = VT::merge(acc1, vm);
+        else acc0 = VT::merge(acc0, vm);
+        // pass 2 recomputes the maximum: keeping this one alive until then
+        // would cost a VGPR per lane-vector
+        asm volatile("" : "+v"(data[j]));
+    };
+    // Threshold from the reports. Every wave finds the 64th largest of its own
+    // report keys (an MSB-first ballot search over the top key bits) and
+    // appends its reports at or above it to an LDS union (at most 64 per
+    // wave); every wave then takes the k-th largest of the union the same way.
+    // Union members are real elements of the slice, so at least k keys reach
+    // the result, and for k <= 64 it is the k-th largest report (to the
+    // searched bits). 1 when the union has fewer than k.
+    auto report_threshold = [&](int call) __attribute__((always_inline)) -> uint32_t {
+        constexpr int NR = 2 * VT::kReports;
+        constexpr int kBits = sizeof(Elem) == 2 ? 16 : 24;
+        uint32_t rep[NR];
+#pragma unroll
+        for (int r = 0; r < VT::kReports; ++r) {
+            const uint32_t b0 = VT::report_bits(acc0, r), b1 = VT::report_bits(acc1, r);
+            const uint32_t k0 = b0 == 0x80000000u ? 0u : raw_order_key(b0);
+            const uint32_t k1 = b1 == 0x80000000u ? 0u : raw_order_key(b1);
+            rep[2 * r] = k0 < valid_min ? 0u : k0;
+            rep[2 * r + 1] = k1 < valid_min ? 0u : k1;
+        }
+        const uint32_t tw = wave_kth<NR, kBits>(rep, 64u);
+        uint32_t n = 0u;
+        uint32_t *u = sm.ukeys[call] + wave * 64u;
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const bool in = rep[r] != 0u && rep[r] >= tw;
+            const uint64_t b = __ballot(in);
+            const uint32_t pos = n + __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+            if (in && pos < 64u) u[pos] = rep[r];
+            n += (uint32_t)__popcll(b);
+        }
+        if (lane == 0u) sm.ucount[call][wave] = min(n, 64u);
+        lds_sync();
+        uint32_t uk[kWaves];
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) uk[w] = lane < sm.ucount[call][w] ? sm.ukeys[call][w * 64 + lane] : 0u;
+        const uint32_t t = wave_kth<kWaves, kBits>(uk, k);
+        return t < 1u ? 1u : t;
+    };
+    uint32_t thr = 1u;
+    bool fast = false, skip_dead = true;
+    // Masked lane-vectors are skipped unless a masked token could still
+    // qualify (greedy rows treat masked tokens as -inf); a positive thr is
+    // tested on the raw signed-integer maximum.
+    auto set_thr = [&](uint32_t t) __attribute__((always_inline)) {
+        thr = t;
+        fast = thr > kZeroKey;
+        skip_dead = sampled || thr > kNegInfKey;
+    };
+    uint32_t has_nan = 0u;  // greedy rows: any NaN selects the reference's lane-structure replay
+    // Pass 2 for lane-vector j with the threshold test fixed at compile time:
+    // FAST for thr above +0 (raw signed-integer maximum), else the order-key
+    // upper bound.
+    auto pass2 = [&](auto fast_tag, int j) __attribute__((always_inline)) {
+        constexpr bool FAST = decltype(fast_tag)::value;
+        if (!sampled) has_nan |= ((uint32_t)j < nval && VT::has_nan(data[j])) ? 1u : 0u;
+        bool go;
+        if constexpr (FAST) {
+            go = ((live[j >> 5] >> (j & 31)) & 1u) && VT::ge_pos(VT::vmax(data[j]), thr);
+        } else {
+            const bool lv = skip_dead ? ((live[j >> 5] >> (j & 31)) & 1u) : ((uint32_t)j < nval);
+            go = lv && VT::upper(data[j]) >= thr;
+        }
+        if (go) {
+            const uint32_t pos = atomicAdd(&sm.flag[2], 1u);
+            if (pos < kStageCap) {
+                s_svec[pos] = data[j];
+                s_sslot[pos] = v0 + wbase + (uint32_t)j * 64u;
+            }
+        }
+        asm volatile("" : "+v"(data[j]));  // as in pass 1: no maximum kept alive
+    };
+    constexpr int NA = NV / 2;
+    static_assert(NV % 8 == 0, "lane-vector count must be a multiple of 8");
+    auto step_in = [&](auto J) __attribute__((always_inline)) {
+        constexpr int j = J;
+        if constexpr (j + D < NV) load(j + D);
+        if constexpr ((j & 7) == 0) flags_at(std::integral_constant<int, j>{});
+        pass1(j);
+    };
+    static_for<0, NA>(step_in);
+    set_thr(report_threshold(0));
+    PHASE_MARK(4);
+    auto second_half = [&](auto fast_tag) __attribute__((always_inline)) {
+        static_for<NA, NV>([&](auto J) __attribute__((always_inline)) {
+            step_in(J);
+            pass2(fast_tag, J - NA);
+            pass2(fast_tag, J);
+        });
+    };
+    if (fast) second_half(std::true_type{});
+    else second_half(std::false_type{});
+    // the V % EPV tail of the last slice, one element per lane (loaded late:
+    // it is rare and holding it across the stream costs a VGPR)
+    const uint32_t tail_bits = has_tail ? f2u(load_elem<Elem>(lrow, tail_id)) : 0u;
+    if (!sampled) {
+        if (has_tail) has_nan |= ((tail_bits & 0x7fffffffu) > 0x7f800000u) ? 1u : 0u;
+        const float pq = P.repetition_penalty + P.frequency_penalty + P.presence_penalty;
+        if (PEN != 0 && !(pq - pq == 0.0f)) has_nan = 1u;  // non-finite penalty parameters
+    }
+    lds_sync();
+    uint32_t nstaged = sm.flag[2];
+    if (nstaged > kStageCap) {
+        // The first half's threshold let too much through (a skewed row):
+        // take the threshold of every report and stage again, reloading the
+        // slice in chunks of 8 lane-vectors (the registers were released as
+        // the stream went).
+        set_thr(report_threshold(1));
+        if (tid == 0) sm.flag[2] = 0u;
+        lds_sync();
+        constexpr int CH = 8;
+        auto restage = [&](auto fast_tag) __attribute__((always_inline)) {
+            static_for<0, NV / CH>([&](auto C) __attribute__((always_inline)) {
+                constexpr int j0 = C * CH, j1 = j0 + CH;
+                static_for<j0, j1>([&](auto J) __attribute__((always_inline)) { load(J); });
+                static_for<j0, j1>([&](auto J) __attribute__((always_inline)) { pass2(fast_tag, J); });
+            });
+        };
+        if (fast) restage(std::true_type{});
+        else restage(std::false_type{});
+        lds_sync();
+        nstaged = sm.flag[2];
+    } else if (nstaged > 128u && nstaged > 2u * k) {
+        // a weak first-half threshold: refine it from every report before
+        // the exact pass (the staged set stays a superset)
+        const uint32_t t = report_threshold(1);
+        if (t > thr) set_thr(t);
+    }
+    PHASE_MARK(5);
+
+    // 5. exact keys of the staged elements (one lane per element), the tail,
+    // and (for penalties that may raise a logit) every penalised token from
+    // the history state
+    auto push = [&](uint32_t key, uint32_t id) __attribute__((always_inline)) {
+        const uint32_t pos = atomicAdd(&sm.flag[1], 1u);
+        if (pos < kStreamCandCap) s_cand[pos] = make_uint2(key, id);
+    };
+    auto count_of = [&](uint32_t id) __attribute__((always_inline)) -> uint32_t {
+        return history ? 1u + hash_lookup(s_hash, a.log2_slots, id) : 1u;
+    };
+    auto pen_key = [&](uint32_t bits, bool allowed, uint32_t count) __attribute__((always_inline)) -> uint32_t {
+        if (!allowed) return masked_key;
+        const float v = configured_logit(u2f(bits), true, count, P.repetition_penalty, P.frequency_penalty,
+                                         P.presence_penalty);
+        const uint32_t key = order_key(v);
+        return key < valid_min ? 0u : key;
+    };
+    // configured key of a token from the vector passes (0: not a candidate;
+    // penalised tokens under raising penalties are left to the history pass)
+    auto elem_key = [&](uint32_t bits, uint32_t id) __attribute__((always_inline)) -> uint32_t {
+        const uint32_t off = id - bm_base;
+        const bool allowed = !mask || ((s_allow[off >> 5] >> (off & 31u)) & 1u);
+        bool pen = false;
+        if constexpr (PEN != 0) pen = (s_pen[off >> 5] >> (off & 31u)) & 1u;
+        if (pen) return lowering ? pen_key(bits, allowed, count_of(id)) : 0u;
+        const uint32_t key = allowed ? raw_order_key(bits) : masked_key;
+        return key < valid_min ? 0u : key;
+    };
+    constexpr uint32_t kLog2Epv = EPV == 8 ? 3u : (EPV == 4 ? 2u : 0u);
+    auto staged_key = [&](uint32_t q) __attribute__((always_inline)) -> uint32_t {
+        const uint32_t i = q >> kLog2Epv, e = q & (uint32_t)(EPV - 1);
+        return elem_key(VT::staged_bits(s_svec, i, e), s_sslot[i] * EPV + e);
+    };
+    auto push_staged = [&]() __attribute__((always_inline)) {
+        if (has_tail) {
+            const uint32_t key = elem_key(tail_bits, tail_id);
+            if (key >= thr && key != 0u) push(key, tail_id);
+        }
+        for (uint32_t q = tid; q < (nstaged << kLog2Epv); q += kBlock) {
+            const uint32_t key = staged_key(q);
+            if (key >= thr && key != 0u) push(key, s_sslot[q >> kLog2Epv] * EPV + (q & (uint32_t)(EPV - 1)));
+        }
+    };
+    if (nstaged > kStageCap) {
+        if (has_tail) {
+            const uint32_t key = elem_key(tail_bits, tail_id);
+            if (key >= thr && key != 0u) push(key, tail_id);
+        }
+    } else {
+        push_staged();
+        if (PEN != 0 && !lowering) {
+            for (uint32_t w = tid; w < bm_n; w += kBlock) {
+                uint32_t bits = s_pen[w];
+                while (bits) {
+                    const uint32_t b = (uint32_t)__builtin_ctz(bits);
+                    bits &= bits - 1u;
+                    const uint32_t id = bm_base + w * 32u + b;
+                    const uint32_t off = id - bm_base;
+                    const bool allowed = !mask || ((s_allow[off >> 5] >> (off & 31u)) & 1u);
+                    const uint32_t key = pen_key(f2u(load_elem<Elem>(lrow, id)), allowed, count_of(id));
+                    if (key >= thr && key != 0u) push(key, id);
+                }
+            }
+        }
+    }
+    {
+        // slice flags: bit 0 = some token allowed, bit 1 = greedy row holds a NaN
+        const uint32_t f = (__ballot(any_allowed != 0u) ? 1u : 0u) | (__ballot(has_nan != 0u) ? 2u : 0u);
+        if (lane == 0u && f) atomicOr(&sm.flag[3], f);
+    }
+    lds_sync();
+    const uint32_t flags_slice = sm.flag[3];
+    if (nstaged <= kStageCap && sm.flag[1] > kStreamCandCap && (PEN == 0 || lowering)) {
+        // Too many candidates for a weak threshold: the exact k-th key of the
+        // staged elements (plus the tail) is a threshold that keeps at least k.
+        lds_sync();
+        const uint32_t n_el = (nstaged << kLog2Epv) + (last_slice ? (uint32_t)(a.vocab - nfull * EPV) : 0u);
+        auto any_key = [&](uint32_t q) __attribute__((always_inline)) -> uint32_t {
+            if (q < (nstaged << kLog2Epv)) return staged_key(q);
+            const uint32_t t = nfull * EPV + (q - (nstaged << kLog2Epv));
+            return elem_key(f2u(load_elem<Elem>(lrow, t)), t);
+        };
+        uint32_t unused_count;
+        const uint32_t t = radix_threshold_fn(0u, n_el, k, sm.hist, sm.sel, unused_count, any_key);
+        set_thr(t > thr ? t : thr);
+        if (tid == 0) sm.flag[1] = 0u;
+        lds_sync();
+        push_staged();
+        lds_sync();
+    }
+    PHASE_MARK(6);
+
+    RowCtx ctx;
+    ctx.logits_row = lrow;
+    ctx.allowed_row = arow;
+    ctx.seen_row = srow;
+    ctx.hash = s_hash;
+    ctx.bitmap = s_pen;
+    ctx.log2_slots = a.log2_slots;
+    ctx.tok0 = bm_base;
+    ctx.rep = P.repetition_penalty;
+    ctx.freq = P.frequency_penalty;
+    ctx.pres = P.presence_penalty;
+    ctx.history = history;
+
+    PHASE_MARK(7);
+
+    // 7. selection -> s_sorted[0 .. n_out)
+    uint32_t C = sm.flag[1];
+    if (tid == 0) {
+        DBG_SET(0, nstaged);
+        DBG_SET(1, C);
+        DBG_SET(2, thr);
+    }
+    if (nstaged > kStageCap || C > kStreamCandCap) {
+        // Skewed slice (for example a constant row): exact selection recomputed
+        // from memory. The k-th largest key kv, then the `need` smallest ids
+        // among keys == kv.
+        auto key_at = [&](uint32_t tt) __attribute__((always_inline)) -> uint32_t {
+            const uint32_t key = order_key(configured_at<Elem>(ctx, tt));
+            return key < valid_min ? 0u : key;
+        };
+        uint32_t count_ge;
+        const uint32_t kv = radix_threshold_fn(tok0, tok1, k, sm.hist, sm.sel, count_ge, key_at);
+        uint32_t gt = 0;
+        for (uint32_t tt = tok0 + tid; tt < tok1; tt += kBlock) gt += key_at(tt) > kv ? 1u : 0u;
+        const uint32_t G = block_sum(gt, sm.scan);
+        const uint32_t need = k > G ? k - G : 0u;
+        auto tie_at = [&](uint32_t tt) __attribute__((always_inline)) -> uint32_t { return key_at(tt) == kv ? ~tt : 0u; };
+        uint32_t ties_ge;
+        const uint32_t id_cut = need ? ~radix_threshold_fn(tok0, tok1, need, sm.hist, sm.sel, ties_ge, tie_at) : 0u;
+        if (tid == 0) sm.flag[1] = 0u;
+        lds_sync();
+        for (uint32_t tt = tok0 + tid; tt < tok1; tt += kBlock) {
+            const uint32_t key = key_at(tt);
+            if (key != 0u && (key > kv || (key == kv && need && tt <= id_cut))) {
+                const uint32_t q = atomicAdd(&sm.flag[1], 1u);
+                if (q < kStreamCandCap) s_cand[q] = make_uint2(key, tt);
+            }
+        }
+        lds_sync();
+        C = min(sm.flag[1], kStreamCandCap);
+    }
+    // Many candidates (a weak threshold): keep the entries at or above the
+    // k-th largest key (LDS radix select) in the staging area, which is free
+    // by now, so the rank sort below stays small.
+    const uint2 *list = s_cand;
+    constexpr uint32_t kTrimCap = stage_area_bytes<Elem, EPV>() / 8u;
+    if (C > 256u && C > 4u * k) {
+        auto cand_key = [&](uint32_t i) __attribute__((always_inline)) -> uint32_t { return s_cand[i].x; };
+        uint32_t unused_count;
+        const uint32_t kth = radix_threshold_fn(0u, C, k, sm.hist, sm.sel, unused_count, cand_key);
+        uint2 *s_trim = (uint2 *)s_svec;
+        if (tid == 0) sm.flag[0] = 0u;
+        lds_sync();
+        for (uint32_t i = tid; i < C; i += kBlock) {
+            const uint2 e = s_cand[i];
+            if (e.x >= kth) {
+                const uint32_t q = atomicAdd(&sm.flag[0], 1u);
+                if (q < kTrimCap) s_trim[q] = e;
+            }
+        }
+        lds_sync();
+        if (sm.flag[0] <= kTrimCap) {
+            list = s_trim;
+            C = sm.flag[0];
+        }
+    }
+    // rank sort (ids are distinct, so ranks are a permutation): G adjacent
+    // lanes share a candidate, each counting the better entries in every G-th
+    // position, and the partial ranks are summed across the group
+    uint32_t G = 1u;
+    while (G < 8u && C * G * 2u <= (uint32_t)kBlock) G <<= 1;
+    for (uint32_t base = 0; base < C * G; base += kBlock) {
+        const uint32_t q = base + tid, i = q / G, part = q % G;
+        uint32_t r = 0;
+        uint2 e = make_uint2(0u, 0u);
+        if (i < C) {
+            e = list[i];
+            uint32_t r1 = 0;
+            uint32_t j = part;
+            for (; j + G < C; j += 2u * G) {
+                r += entry_better(list[j], e) ? 1u : 0u;
+                r1 += entry_better(list[j + G], e) ? 1u : 0u;
+            }
+            if (j < C) r += entry_better(list[j], e) ? 1u : 0u;
+            r += r1;
+        }
+        for (uint32_t o = 1u; o < G; o <<= 1) r += __shfl_xor(r, (int)o, 64);
+        if (i < C && part == 0u && r < k) s_sorted[r] = e;
+    }
+    const uint32_t n_out = C < k ? C : k;
+    lds_sync();
+    PHASE_MARK(8);
+
+    // the sign of a zero survivor comes from its own configured value
+    for (uint32_t i = tid; i < n_out; i += kBlock) {
+        const uint2 e = s_sorted[i];
+        if (e.x == kZeroKey) {
+            const float v = configured_at<Elem>(ctx, e.y);
+            if (f2u(v) == 0x80000000u) s_sorted[i].y = e.y | kNegZeroFlag;
+        }
+    }
+    __syncthreads();
+    PHASE_MARK(9);
+
+    // 8. publish: with several slices the sorted list goes to scratch and the
+    // finish kernel merges the row; a single slice finishes here.
+    if (a.slices > 1) {
+        uint2 *lists = a.scratch_lists + (uint64_t)(row * a.slices + slice) * a.kcap;
+        for (uint32_t i = tid; i < n_out; i += kBlock) lists[i] = s_sorted[i];
+        if (tid == 0) a.scratch_meta[row * a.slices + slice] = n_out | (flags_slice << 16);
+        PHASE_MARK(12);
+        return;
+    }
+    const RowIo io_l = {sm.io[0], sm.io[1], sm.io[2], sm.io[3]};
+    finish_row<Elem, PEN, kBlock>(a, row, io_l, P, k, sampled, n_out, flags_slice, s_sorted, s_big, s_hash, ctx);
+    PHASE_MARK(12);
+}
+
+// Merges the S sorted slice lists of each row (one workgroup per row) and
+// finishes the row. Launched after sample_rows_kernel on the same stream, so
+// the slice lists are visible without any cross-workgroup fence.
+template <typename Elem, int PEN>
+__global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
+    extern __shared__ uint32_t s_dyn[];
+    uint32_t *s_hash = s_dyn;
+    uint2 *s_big = (uint2 *)(s_dyn + a.hash_slots);
+    uint2 *s_sorted = s_big + a.big_entries;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t row = blockIdx.x;
+    const nerve_sampler_row_params P = a.params[row];
+    const RowIo io = load_row_io(a, row);
+    const bool sampled = P.method != NERVE_METHOD_GREEDY;
+    uint32_t k = sampled ? P.top_k : 1u;
+    k = k < 1u ? 1u : (k > a.kcap ? a.kcap : k);
+
+    const uint2 *all = a.scratch_lists + (uint64_t)row * a.slices * a.kcap;
+    const uint32_t *meta = a.scratch_meta + row * a.slices;
+    uint32_t total = 0, row_flags = 0;
+    for (uint32_t s = 0; s < a.slices; ++s) {
+        const uint32_t m = meta[s];
+        total += m & 0xffffu;
+        row_flags |= m >> 16;
+    }
+    const uint32_t ne = a.slices * a.kcap;
+    for (uint32_t i = tid; i < ne; i += kFinishBlock) {
+        const uint32_t s = i / a.kcap, pos = i % a.kcap;
+        if (pos < (meta[s] & 0xffffu)) s_big[i] = all[i];
+    }
+    __syncthreads();
+    // rank of an entry = its position in its own sorted list plus the number
+    // of better entries in every other list (binary search); ids are distinct
+    for (uint32_t i = tid; i < ne; i += kFinishBlock) {
+        const uint32_t s = i / a.kcap, pos = i % a.kcap;
+        if (pos >= (meta[s] & 0xffffu)) continue;
+        const uint2 e = s_big[i];
+        uint32_t r = pos;
+        for (uint32_t o = 0; o < a.slices && r < k; ++o) {
+            if (o == s) continue;
+            const uint2 *lo = s_big + o * a.kcap;
+            uint32_t lo_i = 0, hi_i = meta[o] & 0xffffu;
+            while (lo_i < hi_i) {
+                const uint32_t mid = (lo_i + hi_i) >> 1;
+                if (entry_better(lo[mid], e)) lo_i = mid + 1; else hi_i = mid;
+            }
+            r += lo_i;
+        }
+        if (r < k) s_sorted[r] = e;
+    }
+    const uint32_t n = total < k ? total : k;
+    __syncthreads();
+
+    RowCtx ctx;
+    ctx.logits_row = (const Elem *)a.logits + (uint64_t)row * a.ld;
+    ctx.allowed_row = a.allowed ? a.allowed + (uint64_t)row * a.allowed_stride : nullptr;
+    ctx.seen_row = PEN == 1 ? a.seen + (uint64_t)row * a.seen_stride : nullptr;
+    ctx.hash = s_hash;
+    ctx.bitmap = nullptr;
+    ctx.log2_slots = a.log2_slots;
+    ctx.tok0 = 0;
+    ctx.rep = P.repetition_penalty;
+    ctx.freq = P.frequency_penalty;
+    ctx.pres = P.presence_penalty;
+    ctx.history = PEN == 2;
+    finish_row<Elem, PEN, kFinishBlock>(a, row, io, P, k, sampled, n, row_flags, s_sorted, s_big, s_hash, ctx);
+}
+
+// ---- launch ------------------------------------------------------------------
+
+
+template <typename Elem, int EPV, int NV, int PEN, bool MASK>
+static hipError_t launch_one(const StepArgs &a0, hipStream_t stream) {
+    StepArgs a = a0;
+    auto kern = sample_rows_kernel<Elem, EPV, NV, PEN, MASK>;
+    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)a.dyn_lds_bytes);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(a.batch * a.slices), dim3(kBlock), a.dyn_lds_bytes, stream, a);
+    e = hipGetLastError();
+    if (e != hipSuccess || a.slices == 1u) return e;
+    auto fin = finish_rows_kernel<Elem, PEN>;
+    if (a.finish_lds_bytes > 48u * 1024u) {
+        e = hipFuncSetAttribute((const void *)fin, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)a.finish_lds_bytes);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(fin, dim3(a.batch), dim3(kFinishBlock), a.finish_lds_bytes, stream, a);
+    return hipGetLastError();
+}
+
+template <typename Elem, int EPV, int NV, bool MASK>
+static hipError_t launch_pen_mask(const StepArgs &a, hipStream_t stream) {
+    if (a.history) return launch_one<Elem, EPV, NV, 2, MASK>(a, stream);
+    if (a.seen) return launch_one<Elem, EPV, NV, 1, MASK>(a, stream);
+    return launch_one<Elem, EPV, NV, 0, MASK>(a, stream);
+}
+
+
+// Lane-vectors per lane (NV) of the compiled slice kernels, per variant: the
+// largest keep the whole kernel within 256 VGPRs without spills.
+constexpr uint32_t kBf16NV[] = {8, 16, 24, 32, 40};
+constexpr uint32_t kF32NV[] = {8, 16, 24, 32};
+constexpr uint32_t kScalarNV[] = {16, 32};
+
+template <typename Elem, int EPV, bool MASK>
+static hipError_t launch_vec(const StepArgs &a, hipStream_t stream) {
+    switch (a.nv) {
+        case 8: return launch_pen_mask<Elem, EPV, 8, MASK>(a, stream);
+        case 16: return launch_pen_mask<Elem, EPV, 16, MASK>(a, stream);
+        case 24: return launch_pen_mask<Elem, EPV, 24, MASK>(a, stream);
+        case 32: return launch_pen_mask<Elem, EPV, 32, MASK>(a, stream);
+        case 40:
+            if constexpr (sizeof(Elem) == 2) return launch_pen_mask<Elem, EPV, 40, MASK>(a, stream);
+            return hipErrorInvalidValue;
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <typename Elem, bool MASK>
+static hipError_t launch_scalar(const StepArgs &a, hipStream_t stream) {
+    switch (a.nv) {
+        case 16: return launch_pen_mask<Elem, 1, 16, MASK>(a, stream);
+        case 32: return launch_pen_mask<Elem, 1, 32, MASK>(a, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace nerve

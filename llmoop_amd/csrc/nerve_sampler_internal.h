@@ -61,8 +61,17 @@ uint32_t stream_lds_bytes(uint32_t variant, bool mask, bool pen, uint32_t hash_s
                           uint32_t kcap);
 uint32_t max_vectors_per_lane(uint32_t variant);
 uint32_t vectors_per_lane(uint32_t variant, uint32_t need);  // 0 when need exceeds every kernel
-uint32_t bitmap_words_for(uint32_t variant, uint32_t vec_per_slice);
+uint32_t bitmap_words_for(uint32_t variant, uint32_t nv);  // LDS words of each slice bitmap
 hipError_t launch_sample_rows(uint32_t variant, const StepArgs &a, hipStream_t stream);
+// per-variant slice-kernel launchers (nerve_rows_*.hip)
+hipError_t launch_rows_bf16_plain(const StepArgs &a, hipStream_t stream);
+hipError_t launch_rows_bf16_mask(const StepArgs &a, hipStream_t stream);
+hipError_t launch_rows_f32_plain(const StepArgs &a, hipStream_t stream);
+hipError_t launch_rows_f32_mask(const StepArgs &a, hipStream_t stream);
+hipError_t launch_rows_scalar_bf16_plain(const StepArgs &a, hipStream_t stream);
+hipError_t launch_rows_scalar_bf16_mask(const StepArgs &a, hipStream_t stream);
+hipError_t launch_rows_scalar_f32_plain(const StepArgs &a, hipStream_t stream);
+hipError_t launch_rows_scalar_f32_mask(const StepArgs &a, hipStream_t stream);
 hipError_t launch_record_tokens(uint32_t *seen, uint32_t seen_stride, uint32_t rows, const uint32_t *ids,
                                 uint32_t ids_stride, const uint32_t *counts, uint32_t max_count, uint32_t vocab,
                                 hipStream_t stream);
