@@ -548,6 +548,7 @@ struct SharedSmall {
     uint32_t io[4];                  // the row's RowIo, stored during the set-up
     uint32_t ukeys[2][kWaves * 64];  // report unions of the two threshold passes
     uint32_t ucount[2][kWaves];
+    uint32_t uthr[2];
 };
 
 __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t n) {
@@ -919,7 +920,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     };
     // lane-vectors in flight ahead of the one being processed
 #ifndef NERVE_LOOKAHEAD
-#define NERVE_LOOKAHEAD 16
+#define NERVE_LOOKAHEAD 6
 #endif
     constexpr int D = NV < NERVE_LOOKAHEAD ? NV : NERVE_LOOKAHEAD;
     static_for<0, D>([&](auto J) __attribute__((always_inline)) { load(J); });
@@ -1054,43 +1055,42 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         // would cost a VGPR per lane-vector
         asm volatile("" : "+v"(data[j]));
     };
-    // Threshold from the reports. Every wave finds the 64th largest of its own
-    // report keys (an MSB-first ballot search over the top key bits) and
-    // appends its reports at or above it to an LDS union (at most 64 per
-    // wave); every wave then takes the k-th largest of the union the same way.
-    // Union members are real elements of the slice, so at least k keys reach
-    // the result, and for k <= 64 it is the k-th largest report (to the
+    // Threshold from the reports. A lane reports the largest key among its
+    // accumulated elements (itself an element of the slice). Every wave finds
+    // the min(k, 64)-th largest report of its lanes by an MSB-first ballot
+    // search over the top key bits and appends the reports at or above it to
+    // an LDS union (at most 64 per wave); wave 0 takes the k-th largest of the
+    // union the same way and publishes it. At least k elements of the slice
+    // reach the result, and for k <= 64 it is the k-th largest report (to the
     // searched bits). 1 when the union has fewer than k.
     auto report_threshold = [&](int call) __attribute__((always_inline)) -> uint32_t {
-        constexpr int NR = 2 * VT::kReports;
         constexpr int kBits = sizeof(Elem) == 2 ? 16 : 24;
-        uint32_t rep[NR];
+        uint32_t best[1] = {0u};
 #pragma unroll
         for (int r = 0; r < VT::kReports; ++r) {
             const uint32_t b0 = VT::report_bits(acc0, r), b1 = VT::report_bits(acc1, r);
-            const uint32_t k0 = b0 == 0x80000000u ? 0u : raw_order_key(b0);
-            const uint32_t k1 = b1 == 0x80000000u ? 0u : raw_order_key(b1);
-            rep[2 * r] = k0 < valid_min ? 0u : k0;
-            rep[2 * r + 1] = k1 < valid_min ? 0u : k1;
+            uint32_t k0 = b0 == 0x80000000u ? 0u : raw_order_key(b0);
+            uint32_t k1 = b1 == 0x80000000u ? 0u : raw_order_key(b1);
+            k0 = k0 < valid_min ? 0u : k0;
+            k1 = k1 < valid_min ? 0u : k1;
+            best[0] = max(best[0], max(k0, k1));
         }
-        const uint32_t tw = wave_kth<NR, kBits>(rep, 64u);
-        uint32_t n = 0u;
-        uint32_t *u = sm.ukeys[call] + wave * 64u;
-#pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            const bool in = rep[r] != 0u && rep[r] >= tw;
-            const uint64_t b = __ballot(in);
-            const uint32_t pos = n + __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
-            if (in && pos < 64u) u[pos] = rep[r];
-            n += (uint32_t)__popcll(b);
-        }
-        if (lane == 0u) sm.ucount[call][wave] = min(n, 64u);
+        const uint32_t tw = wave_kth<1, kBits>(best, min(k, 64u));
+        const bool in = best[0] != 0u && best[0] >= tw;
+        const uint64_t bal = __ballot(in);
+        const uint32_t pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+        if (in) sm.ukeys[call][wave * 64u + pos] = best[0];
+        if (lane == 0u) sm.ucount[call][wave] = (uint32_t)__popcll(bal);
         lds_sync();
-        uint32_t uk[kWaves];
+        if (wave == 0u) {
+            uint32_t uk[kWaves];
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) uk[w] = lane < sm.ucount[call][w] ? sm.ukeys[call][w * 64 + lane] : 0u;
-        const uint32_t t = wave_kth<kWaves, kBits>(uk, k);
-        return t < 1u ? 1u : t;
+            for (int w = 0; w < kWaves; ++w) uk[w] = lane < sm.ucount[call][w] ? sm.ukeys[call][w * 64 + lane] : 0u;
+            const uint32_t t = wave_kth<kWaves, kBits>(uk, k);
+            if (lane == 0u) sm.uthr[call] = t < 1u ? 1u : t;
+        }
+        lds_sync();
+        return sm.uthr[call];
     };
     uint32_t thr = 1u;
     bool fast = false, skip_dead = true;
@@ -1354,6 +1354,20 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     // rank sort (ids are distinct, so ranks are a permutation): G adjacent
     // lanes share a candidate, each counting the better entries in every G-th
     // position, and the partial ranks are summed across the group
+    if (C <= 128u) {
+        // the common case, unrolled: every comparison's read is issued at once
+        const uint32_t G = C <= 64u ? 8u : 4u;
+        const uint32_t i = tid / G, part = tid % G;
+        const uint2 e = i < C ? list[i] : make_uint2(0u, 0u);
+        uint32_t r = 0;
+        uint2 o[32];
+        static_for<0, 32>([&](auto T) __attribute__((always_inline)) { o[T] = list[part + G * (uint32_t)T]; });
+        static_for<0, 32>([&](auto T) __attribute__((always_inline)) {
+            r += (part + G * (uint32_t)T < C && entry_better(o[T], e)) ? 1u : 0u;
+        });
+        for (uint32_t off = 1u; off < G; off <<= 1) r += __shfl_xor(r, (int)off, 64);
+        if (i < C && part == 0u && r < k) s_sorted[r] = e;
+    } else {
     uint32_t G = 1u;
     while (G < 8u && C * G * 2u <= (uint32_t)kBlock) G <<= 1;
     for (uint32_t base = 0; base < C * G; base += kBlock) {
@@ -1373,6 +1387,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         }
         for (uint32_t o = 1u; o < G; o <<= 1) r += __shfl_xor(r, (int)o, 64);
         if (i < C && part == 0u && r < k) s_sorted[r] = e;
+    }
     }
     const uint32_t n_out = C < k ? C : k;
     lds_sync();

@@ -18,7 +18,9 @@ from dataclasses import dataclass, field
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libnerve_sampler.so")
+# NERVE_SAMPLER_LIBRARY selects another build of the same library (for
+# example one compiled with different launch parameters)
+LIB_PATH = os.environ.get("NERVE_SAMPLER_LIBRARY") or os.path.join(HERE, "libnerve_sampler.so")
 
 NERVE_OK = 0
 ERR_INVALID_LOGITS_BYTE_CAPACITY = 1
