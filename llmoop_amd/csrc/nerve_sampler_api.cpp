@@ -334,7 +334,7 @@ int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *str
     if (slices * d.top_k_capacity > big) big = slices * d.top_k_capacity;
     if (d.top_k_capacity + 32u > big) big = d.top_k_capacity + 32u;  // weights + running sums of the finish step
     a.big_entries = big;
-    a.finish_lds_bytes = a.hash_slots * 4u + big * 8u + d.top_k_capacity * 8u;
+    a.finish_lds_bytes = a.hash_slots * 4u + big * 8u + d.top_k_capacity * 8u + (d.top_k_capacity + 64u) * 4u;
     const uint32_t stream_lds = nerve::stream_lds_bytes(variant, b->allowed != nullptr, pen, a.hash_slots,
                                                         a.bitmap_words, d.top_k_capacity);
     a.dyn_lds_bytes = stream_lds;

@@ -549,6 +549,7 @@ struct SharedSmall {
     uint32_t ukeys[2][kWaves * 64];  // report unions of the two threshold passes
     uint32_t ucount[2][kWaves];
     uint32_t uthr[2];
+    uint32_t maxkey;
 };
 
 __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t n) {
@@ -593,11 +594,12 @@ __device__ __forceinline__ RowIo load_row_io(const StepArgs &a, uint32_t row) {
 template <typename Elem, int PEN, int NT>
 __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, const RowIo &io, const nerve_sampler_row_params &P, uint32_t k,
                            bool sampled, uint32_t n, uint32_t row_flags, uint2 *s_sorted, uint2 *s_big,
-                           uint32_t *s_hash, const RowCtx &ctx) {
+                           float *s_w, float *s_p, uint32_t *s_hash, const RowCtx &ctx) {
+    // s_w [kcap + 64]: the weights of s_sorted[0 .. n), written by the caller
+    // (the rest are computed here), then zero past the min-p cut.
+    // s_p [kcap]: running sums, then probabilities.
     __shared__ uint32_t s_res[2];
     const uint32_t tid = threadIdx.x;
-    float *s_w = (float *)s_big;                 // [kcap + 64] weights, zero past the min-p cut
-    float *s_p = (float *)s_big + a.kcap + 64u;  // [kcap] running sums, then probabilities
     uint32_t token = 0, sel_bits = 0, out_flags = 0, kout = 1;
     uint32_t *sc = a.stream_control ? a.stream_control + (uint64_t)row * 5u : nullptr;
 
@@ -692,7 +694,8 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
                 if (below) n_valid = min(n_valid, c0 + (uint32_t)__builtin_ctzll(below));
                 if (c0 >= n_valid) break;
                 const bool in = i < n_valid;
-                s_w[i] = in ? nerve_expf(v / T - m) : 0.0f;
+                const float w = i < n ? s_w[i] : nerve_expf(v / T - m);
+                s_w[i] = in ? w : 0.0f;
                 PHASE_MARK(14);
                 float wv[64];
                 static_for<0, 64>([&](auto J) __attribute__((always_inline)) { wv[J] = s_w[c0 + (uint32_t)J]; });
@@ -809,21 +812,24 @@ __host__ __device__ constexpr uint32_t slice_bitmap_words(uint32_t tokens, uint3
 // PEN: 0 = no penalty state, 1 = seen bitmap (set semantics), 2 = history ids
 // (count semantics). EPV elements per lane-vector, NV lane-vectors per lane.
 //
-// The slice [v0, v1) of full lane-vectors lives in VGPRs: wave w owns slots
-// v0 + w * 64 * NV + [0, 64 * NV), and lane-vector j of lane l is the slot
-// 64 * j + l of that run. Every load is issued before any selection work, then
-//   pass 1  as the loads land, two signed-integer maxima per lane over the
-//           lane-vectors with no penalty state and no masked element; every
-//           report is a real element, so the k-th largest report key is a
-//           lower bound of the slice's k-th largest configured key;
-//   select  that k-th largest report (LDS radix select) -> thr;
+// The slice [v0, v1) of full lane-vectors lives in VGPRs: wave w owns a run
+// of `span` slots, and lane-vector j of lane l is the slot 64 * j + l of that
+// run. Loads run D lane-vectors ahead of the processing:
+//   pass 1  as the loads land, two signed-integer maxima per lane over the raw
+//           values of fully allowed lane-vectors; each report is a real
+//           element of the slice;
+//   select  after the first half: every wave's top reports go to an LDS union
+//           and its k-th largest key becomes thr;
 //   pass 2  lane-vectors whose raw maximum reaches thr are staged in LDS;
-//   exact   one lane per staged lane-vector computes configured keys and
-//           appends keys >= thr to the candidate list.
-// Penalties that never raise a logit (repetition >= 1, frequency and presence
-// >= 0) keep configured <= raw, so the raw test is conservative for penalised
-// tokens too. Other settings take penalised tokens out of the vector passes
-// and evaluate each one from the history table instead (one gather per id).
+//   exact   one lane per staged element computes its configured key (mask,
+//           penalties) and appends keys >= thr to the candidate list.
+// The top k are all candidates exactly when at least k configured keys reach
+// thr; a slice where penalties pushed too many reported values below thr
+// takes the exact selection from memory instead. Penalties that never raise
+// a logit (repetition >= 1, frequency and presence >= 0) keep configured <=
+// raw, so the raw test of pass 2 is conservative for penalised tokens too.
+// Other settings take penalised tokens out of the vector passes and evaluate
+// each one from the history state instead (one gather per id).
 template <typename Elem, int EPV, int NV, int PEN, bool MASK>
 __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     constexpr int HPT = (kMaxHistory + kBlock - 1) / kBlock;  // history ids per lane
@@ -938,6 +944,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         sm.flag[1] = 0u;  // candidates
         sm.flag[2] = 0u;  // staged lane-vectors
         sm.flag[3] = 0u;  // slice flags
+        sm.maxkey = 0u;   // largest candidate key
         sm.ones[0] = 0xffffffffu;
         sm.io[0] = io.seed;
         sm.io[1] = io.tick_lo;
@@ -963,39 +970,46 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             }
         }
     }
-    if constexpr (PEN == 1) {
-#pragma unroll
-        for (int i = 0; i < BW; ++i) {
-            const uint32_t w = tid + (uint32_t)i * kBlock;
-            if (w < bm_n) s_pen[w] = sw[i] & range_bits(w);
-        }
-    }
     lds_sync();
-    if constexpr (history) {
-        uint32_t first[HPT];
+    // The penalty state (seen words, or history ids -> bitmap + repeat table)
+    // is needed only by the exact pass after the stream, so it is built at the
+    // midpoint of the stream, when its loads have long landed.
+    auto build_penalty_state = [&]() __attribute__((always_inline)) {
+        if constexpr (PEN == 1) {
 #pragma unroll
-        for (int h = 0; h < HPT; ++h) {
-            const uint32_t id = hist[h];
-            first[h] = 0xffffffffu;
-            if (tid + (uint32_t)h * kBlock < hlen && id >= tok0 && id < tok1) {
-                const uint32_t o = id - bm_base;
-                first[h] = atomicOr(&s_pen[o >> 5], 1u << (o & 31u)) & (1u << (o & 31u));
+            for (int i = 0; i < BW; ++i) {
+                const uint32_t w = tid + (uint32_t)i * kBlock;
+                if (w < bm_n) s_pen[w] = sw[i] & range_bits(w);
             }
         }
+        if constexpr (history) {
+            uint32_t first[HPT];
 #pragma unroll
-        for (int h = 0; h < HPT; ++h)
-            if (first[h] != 0xffffffffu && first[h] != 0u) hash_insert(s_hash, a.log2_slots, hist[h]);
-        lds_sync();
-    }
+            for (int h = 0; h < HPT; ++h) {
+                const uint32_t id = hist[h];
+                first[h] = 0xffffffffu;
+                if (tid + (uint32_t)h * kBlock < hlen && id >= tok0 && id < tok1) {
+                    const uint32_t o = id - bm_base;
+                    first[h] = atomicOr(&s_pen[o >> 5], 1u << (o & 31u)) & (1u << (o & 31u));
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < HPT; ++h)
+                if (first[h] != 0xffffffffu && first[h] != 0u) hash_insert(s_hash, a.log2_slots, hist[h]);
+        }
+    };
     PHASE_MARK(2);
 
     // 3. the stream. Lane-vector j is processed as it lands while lane-vector
-    // j + D is issued. Per group of 8: the flags from the LDS bitmaps (ok =
-    // every element valid, allowed and free of penalty state; live = some
-    // element valid and allowed). Pass 1 folds ok lane-vectors into the lane
-    // reports. After the first half, thr (a lower bound of the slice's k-th
-    // largest key, from the reports so far) is set and pass 2 stages every
-    // lane-vector that can hold a key >= thr, first-half ones included.
+    // j + D is issued. With a mask, per group of 8: the flags from the mask
+    // bitmap (ok = every element valid and allowed; live = some element valid
+    // and allowed); without one, every valid lane-vector is ok and live. Pass
+    // 1 folds the raw values of ok lane-vectors into the lane reports. After
+    // the first half, thr is set from the reports so far and pass 2 stages
+    // every lane-vector that can hold a key >= thr, first-half ones included.
+    // Raw reports ignore penalties, so thr is a guess, checked after the exact
+    // pass: the top k are all candidates exactly when at least k keys reach
+    // thr; otherwise the slice takes the exact selection from memory.
     const uint32_t nval = wslots > lane ? (wslots - lane + 63u) / 64u : 0u;  // valid lane-vectors of this lane
     uint32_t okm[LW], live[LW], vmask[LW];
 #pragma unroll
@@ -1012,37 +1026,27 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     // the reads of invalid ones stay inside them (their flags are masked).
     const uint32_t tok_base = (v0 + wbase) * EPV - bm_base;
     const uint32_t wsh = tok_base & 31u;
-    const uint32_t *pen_w = s_pen + (tok_base >> 5);
     const uint32_t *allow_w = s_allow + (tok_base >> 5);
     constexpr uint32_t kWordsPerJ = 64u * EPV / 32u;
     auto flags_group = [&](auto mask_tag, auto J0) __attribute__((always_inline)) {
         constexpr bool M = decltype(mask_tag)::value;
         constexpr int j0 = decltype(J0)::value;
-        uint32_t aw[8], pw[8];
+        uint32_t aw[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            if constexpr (M) aw[q] = allow_w[(uint32_t)(j0 + q) * kWordsPerJ];
-            if constexpr (PEN != 0) pw[q] = pen_w[(uint32_t)(j0 + q) * kWordsPerJ];
-        }
+        for (int q = 0; q < 8; ++q) aw[q] = allow_w[(uint32_t)(j0 + q) * kWordsPerJ];
         uint32_t okg = 0u, lvg = 0u;
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            bool ok = true, lv = true;
-            if constexpr (M) {
-                const uint32_t ab = (aw[q] >> wsh) & kFull;
-                ok = ab == kFull;
-                lv = ab != 0u;
-            }
-            if constexpr (PEN != 0) ok = ok && ((pw[q] >> wsh) & kFull) == 0u;
-            okg |= ok ? (1u << q) : 0u;
-            lvg |= lv ? (1u << q) : 0u;
+            const uint32_t ab = (aw[q] >> wsh) & kFull;
+            okg |= ab == kFull ? (1u << q) : 0u;
+            lvg |= ab != 0u ? (1u << q) : 0u;
         }
         const int sh = j0 & 31;
         okm[j0 >> 5] &= ~(0xffu << sh) | (okg << sh);
         live[j0 >> 5] &= ~(0xffu << sh) | (lvg << sh);
     };
     auto flags_at = [&](auto J0) __attribute__((always_inline)) {
-        if constexpr (MASK || PEN != 0) flags_group(std::integral_constant<bool, MASK>{}, J0);
+        if constexpr (MASK) flags_group(std::true_type{}, J0);
     };
     uint32_t acc0 = VT::kAccInit, acc1 = VT::kAccInit;
     auto pass1 = [&](int j) __attribute__((always_inline)) {
@@ -1135,6 +1139,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     };
     static_for<0, NA>(step_in);
     set_thr(report_threshold(0));
+    build_penalty_state();
     PHASE_MARK(4);
     auto second_half = [&](auto fast_tag) __attribute__((always_inline)) {
         static_for<NA, NV>([&](auto J) __attribute__((always_inline)) {
@@ -1189,6 +1194,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     auto push = [&](uint32_t key, uint32_t id) __attribute__((always_inline)) {
         const uint32_t pos = atomicAdd(&sm.flag[1], 1u);
         if (pos < kStreamCandCap) s_cand[pos] = make_uint2(key, id);
+        atomicMax(&sm.maxkey, key);
     };
     auto count_of = [&](uint32_t id) __attribute__((always_inline)) -> uint32_t {
         return history ? 1u + hash_lookup(s_hash, a.log2_slots, id) : 1u;
@@ -1297,10 +1303,11 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         DBG_SET(1, C);
         DBG_SET(2, thr);
     }
-    if (nstaged > kStageCap || C > kStreamCandCap) {
-        // Skewed slice (for example a constant row): exact selection recomputed
-        // from memory. The k-th largest key kv, then the `need` smallest ids
-        // among keys == kv.
+    if (nstaged > kStageCap || C > kStreamCandCap || (C < k && thr > 1u)) {
+        // Skewed slice (for example a constant row), or penalties that pushed
+        // more than C - k of the reported values below thr: exact selection
+        // recomputed from memory. The k-th largest key kv, then the `need`
+        // smallest ids among keys == kv.
         auto key_at = [&](uint32_t tt) __attribute__((always_inline)) -> uint32_t {
             const uint32_t key = order_key(configured_at<Elem>(ctx, tt));
             return key < valid_min ? 0u : key;
@@ -1321,6 +1328,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             if (key != 0u && (key > kv || (key == kv && need && tt <= id_cut))) {
                 const uint32_t q = atomicAdd(&sm.flag[1], 1u);
                 if (q < kStreamCandCap) s_cand[q] = make_uint2(key, tt);
+                atomicMax(&sm.maxkey, key);
             }
         }
         lds_sync();
@@ -1330,7 +1338,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     // k-th largest key (LDS radix select) in the staging area, which is free
     // by now, so the rank sort below stays small.
     const uint2 *list = s_cand;
-    constexpr uint32_t kTrimCap = stage_area_bytes<Elem, EPV>() / 8u;
+    constexpr uint32_t kTrimCap = kStageCap * (uint32_t)sizeof(vec_t) / 8u;
     if (C > 256u && C > 4u * k) {
         auto cand_key = [&](uint32_t i) __attribute__((always_inline)) -> uint32_t { return s_cand[i].x; };
         uint32_t unused_count;
@@ -1351,6 +1359,18 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             C = sm.flag[0];
         }
     }
+    // The writer of rank r also settles the sign of a zero survivor (from its
+    // own configured value) and, for sampled rows, computes its weight
+    // exp(l / T - m) with m = l0 / T from the largest candidate key (the sign
+    // of a zero l cannot change a weight).
+    float *s_wt = (float *)s_sslot;  // [kcap + 64], the staging slots are free by now
+    const float T = P.temperature;
+    const float m_w = sampled ? key_to_float(sm.maxkey) / T : 0.0f;
+    auto emit = [&](uint32_t r, uint2 e) __attribute__((always_inline)) {
+        if (e.x == kZeroKey && f2u(configured_at<Elem>(ctx, e.y)) == 0x80000000u) e.y |= kNegZeroFlag;
+        s_sorted[r] = e;
+        if (sampled && a.slices == 1u) s_wt[r] = nerve_expf(entry_value(e) / T - m_w);
+    };
     // rank sort (ids are distinct, so ranks are a permutation): G adjacent
     // lanes share a candidate, each counting the better entries in every G-th
     // position, and the partial ranks are summed across the group
@@ -1359,14 +1379,17 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         const uint32_t G = C <= 64u ? 8u : 4u;
         const uint32_t i = tid / G, part = tid % G;
         const uint2 e = i < C ? list[i] : make_uint2(0u, 0u);
+        // (key, ~id) as one unsigned 64-bit value orders like entry_better
+        const uint64_t pe = ((uint64_t)e.x << 32) | (uint64_t)(~e.y);
         uint32_t r = 0;
         uint2 o[32];
-        static_for<0, 32>([&](auto T) __attribute__((always_inline)) { o[T] = list[part + G * (uint32_t)T]; });
-        static_for<0, 32>([&](auto T) __attribute__((always_inline)) {
-            r += (part + G * (uint32_t)T < C && entry_better(o[T], e)) ? 1u : 0u;
+        static_for<0, 32>([&](auto J) __attribute__((always_inline)) { o[J] = list[part + G * (uint32_t)J]; });
+        static_for<0, 32>([&](auto J) __attribute__((always_inline)) {
+            const uint64_t po = ((uint64_t)o[J].x << 32) | (uint64_t)(~o[J].y);
+            r += (part + G * (uint32_t)J < C && po > pe) ? 1u : 0u;
         });
         for (uint32_t off = 1u; off < G; off <<= 1) r += __shfl_xor(r, (int)off, 64);
-        if (i < C && part == 0u && r < k) s_sorted[r] = e;
+        if (i < C && part == 0u && r < k) emit(r, e);
     } else {
     uint32_t G = 1u;
     while (G < 8u && C * G * 2u <= (uint32_t)kBlock) G <<= 1;
@@ -1386,23 +1409,13 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             r += r1;
         }
         for (uint32_t o = 1u; o < G; o <<= 1) r += __shfl_xor(r, (int)o, 64);
-        if (i < C && part == 0u && r < k) s_sorted[r] = e;
+        if (i < C && part == 0u && r < k) emit(r, e);
     }
     }
     const uint32_t n_out = C < k ? C : k;
     lds_sync();
     PHASE_MARK(8);
 
-    // the sign of a zero survivor comes from its own configured value
-    for (uint32_t i = tid; i < n_out; i += kBlock) {
-        const uint2 e = s_sorted[i];
-        if (e.x == kZeroKey) {
-            const float v = configured_at<Elem>(ctx, e.y);
-            if (f2u(v) == 0x80000000u) s_sorted[i].y = e.y | kNegZeroFlag;
-        }
-    }
-    __syncthreads();
-    PHASE_MARK(9);
 
     // 8. publish: with several slices the sorted list goes to scratch and the
     // finish kernel merges the row; a single slice finishes here.
@@ -1414,7 +1427,8 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         return;
     }
     const RowIo io_l = {sm.io[0], sm.io[1], sm.io[2], sm.io[3]};
-    finish_row<Elem, PEN, kBlock>(a, row, io_l, P, k, sampled, n_out, flags_slice, s_sorted, s_big, s_hash, ctx);
+    finish_row<Elem, PEN, kBlock>(a, row, io_l, P, k, sampled, n_out, flags_slice, s_sorted, s_big, s_wt,
+                                  (float *)s_big + 64, s_hash, ctx);
     PHASE_MARK(12);
 }
 
@@ -1427,6 +1441,7 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
     uint32_t *s_hash = s_dyn;
     uint2 *s_big = (uint2 *)(s_dyn + a.hash_slots);
     uint2 *s_sorted = s_big + a.big_entries;
+    float *s_wt = (float *)(s_sorted + a.kcap);  // [kcap + 64] weights of the merged list
     const uint32_t tid = threadIdx.x;
     const uint32_t row = blockIdx.x;
     const nerve_sampler_row_params P = a.params[row];
@@ -1437,12 +1452,15 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
 
     const uint2 *all = a.scratch_lists + (uint64_t)row * a.slices * a.kcap;
     const uint32_t *meta = a.scratch_meta + row * a.slices;
-    uint32_t total = 0, row_flags = 0;
+    uint32_t total = 0, row_flags = 0, maxkey = 0;
     for (uint32_t s = 0; s < a.slices; ++s) {
         const uint32_t m = meta[s];
         total += m & 0xffffu;
         row_flags |= m >> 16;
+        if (m & 0xffffu) maxkey = max(maxkey, all[(uint64_t)s * a.kcap].x);  // the head of a sorted list
     }
+    const float T = P.temperature;
+    const float m_w = sampled ? key_to_float(maxkey) / T : 0.0f;
     const uint32_t ne = a.slices * a.kcap;
     for (uint32_t i = tid; i < ne; i += kFinishBlock) {
         const uint32_t s = i / a.kcap, pos = i % a.kcap;
@@ -1466,7 +1484,10 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
             }
             r += lo_i;
         }
-        if (r < k) s_sorted[r] = e;
+        if (r < k) {
+            s_sorted[r] = e;
+            if (sampled) s_wt[r] = nerve_expf(entry_value(e) / T - m_w);
+        }
     }
     const uint32_t n = total < k ? total : k;
     __syncthreads();
@@ -1483,7 +1504,8 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
     ctx.freq = P.frequency_penalty;
     ctx.pres = P.presence_penalty;
     ctx.history = PEN == 2;
-    finish_row<Elem, PEN, kFinishBlock>(a, row, io, P, k, sampled, n, row_flags, s_sorted, s_big, s_hash, ctx);
+    finish_row<Elem, PEN, kFinishBlock>(a, row, io, P, k, sampled, n, row_flags, s_sorted, s_big, s_wt, (float *)s_big,
+                                        s_hash, ctx);
 }
 
 // ---- launch ------------------------------------------------------------------

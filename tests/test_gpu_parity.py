@@ -170,3 +170,38 @@ def test_benchmark_configs_full_size(oracle, name):
         empty = w.extra["empty_rows"]
         assert (gpu["token_id"][empty] == 2).all()
         assert (gpu["flags"][empty] == 3).all()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_penalised_top_tokens_take_the_exact_path(oracle, dtype):
+    """The top raw logits of each row are all in its history with a large
+    repetition penalty: the lane reports (raw values) point at tokens whose
+    configured values fall far below, so fewer than k candidates reach the
+    report threshold and the slice must fall back to the exact selection."""
+    from llmoop_amd.workloads import to_bf16_bits
+
+    rng = np.random.default_rng(31)
+    B, V, H = 8, 40000, 256
+    x = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    hist = np.zeros((B, H), np.uint32)
+    for r in range(B):
+        top = np.argsort(-x[r])[:150]
+        hist[r, :150] = top
+        hist[r, 150:] = rng.integers(0, V, H - 150)
+    logits = to_bf16_bits(x) if dtype == "bf16" else x
+    params = _random_params(rng, B, 64, method=1)
+    params["top_k"] = 50
+    params["repetition_penalty"] = 50.0
+    params["frequency_penalty"] = 0.0
+    params["presence_penalty"] = 0.0
+    params["min_p"] = 0.0
+    kw = dict(history=hist, history_len=np.full(B, H, np.uint32),
+              seeds=rng.integers(0, 2**32, B, dtype=np.uint64).astype(np.uint32),
+              steps=rng.integers(0, 2**40, B, dtype=np.uint64))
+    _say(f"penalised top tokens {dtype}")
+    ref = oracle.sample(logits, params, top_k_capacity=64, **kw)
+    gpu = run_gpu(logits, params, top_k_capacity=64, **kw)
+    assert_parity(gpu, ref, params, label="penalised-top", prob_rtol=1e-5 if dtype == "f32" else 2e-3)
+    # no survivor is one of the penalised top tokens
+    for r in range(B):
+        assert not set(gpu["topk_ids"][r][:50]) & set(hist[r, :150].tolist())
