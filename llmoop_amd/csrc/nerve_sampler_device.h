@@ -679,59 +679,93 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
                 minimum = l0 + d;
             }
             PHASE_MARK(13);
-            // Per chunk of 64 survivors: the min-p cut (the first survivor
-            // below the floor ends the list), the weights, and the running
-            // sums in the reference's sequential order: lane i adds w_c0,
-            // w_c0+1, ... in turn and +0.0 (exact) for the terms after its own,
-            // so its sum is the reference's prefix sum P_i, rounding for
-            // rounding. s_w is zero past the cut.
-            uint32_t n_valid = k;
-            float carry = 0.0f;  // P_(c0 - 1)
-            for (uint32_t c0 = 0; c0 < n_valid; c0 += 64u) {
-                const uint32_t i = c0 + lane;
-                const float v = i < k ? entry_value(s_sorted[i]) : 0.0f;
-                const uint64_t below = __ballot(i < k && v < minimum);
-                if (below) n_valid = min(n_valid, c0 + (uint32_t)__builtin_ctzll(below));
-                if (c0 >= n_valid) break;
-                const bool in = i < n_valid;
-                const float w = i < n ? s_w[i] : nerve_expf(v / T - m);
-                s_w[i] = in ? w : 0.0f;
-                PHASE_MARK(14);
+            // The min-p cut (the first survivor below the floor ends the
+            // list), then running sums in the reference's sequential order:
+            // lane i adds w_0, w_1, ... in turn and +0.0 (exact) for the terms
+            // after its own, so its sum is the reference's prefix sum P_i,
+            // rounding for rounding.
+            uint32_t n_valid = k, nucleus, selected;
+            float nucleus_weight;
+            if (k <= 64u) {
+                // one survivor per lane: values, weights and sums in registers
+                const bool live = lane < k;
+                const float v = live ? entry_value(s_sorted[lane]) : 0.0f;
+                const uint64_t below = __ballot(live && v < minimum);
+                if (below) n_valid = (uint32_t)__builtin_ctzll(below);
+                float w = 0.0f;
+                if (live) {
+                    if (lane < n) {
+                        w = s_w[lane];
+                    } else {
+                        w = nerve_expf(v / T - m);  // padding entries
+                        s_w[lane] = w;
+                    }
+                }
                 float wv[64];
-                static_for<0, 64>([&](auto J) __attribute__((always_inline)) { wv[J] = s_w[c0 + (uint32_t)J]; });
-                float acc = carry;
+                static_for<0, 64>([&](auto J) __attribute__((always_inline)) { wv[J] = s_w[(uint32_t)J]; });
+                float acc = 0.0f;
                 static_for<0, 64>([&](auto J) __attribute__((always_inline)) {
-                    acc = acc + ((uint32_t)J <= lane ? wv[J] : 0.0f);
+                    if ((uint32_t)J < n_valid) acc = acc + ((uint32_t)J <= lane ? wv[J] : 0.0f);
                 });
-                s_p[i] = acc;
-                carry = u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(min(64u, n_valid - c0) - 1u)));
-            }
-            PHASE_MARK(10);
-            const float total = n_valid ? carry : 0.0f;
-            const float threshold = P.top_p * total;
-            uint32_t nucleus = n_valid;
-            for (uint32_t c0 = 0; c0 < n_valid; c0 += 64u) {
-                const uint32_t i = c0 + lane;
-                const uint64_t b = __ballot(i < n_valid && s_p[i] >= threshold);
-                if (b) {
-                    nucleus = c0 + (uint32_t)__builtin_ctzll(b) + 1u;
-                    break;
+                PHASE_MARK(10);
+                const float total = n_valid ? u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(n_valid - 1u))) : 0.0f;
+                const float threshold = P.top_p * total;
+                const uint64_t bn = __ballot(lane < n_valid && acc >= threshold);
+                nucleus = bn ? (uint32_t)__builtin_ctzll(bn) + 1u : n_valid;
+                if (nucleus == 0u) nucleus = 1u;
+                nucleus_weight = n_valid ? u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(nucleus - 1u))) : 0.0f;
+                PHASE_MARK(15);
+                const float target = u * nucleus_weight;
+                const uint64_t bs = __ballot(lane < nucleus && lane < n_valid && target < acc);
+                selected = bs ? (uint32_t)__builtin_ctzll(bs) : nucleus - 1u;
+                if (live) s_p[lane] = (lane < nucleus && lane < n_valid) ? w / nucleus_weight : 0.0f;
+            } else {
+                // chunks of 64 survivors; s_w is zeroed past the cut
+                float carry = 0.0f;  // P_(c0 - 1)
+                for (uint32_t c0 = 0; c0 < n_valid; c0 += 64u) {
+                    const uint32_t i = c0 + lane;
+                    const float v = i < k ? entry_value(s_sorted[i]) : 0.0f;
+                    const uint64_t below = __ballot(i < k && v < minimum);
+                    if (below) n_valid = min(n_valid, c0 + (uint32_t)__builtin_ctzll(below));
+                    if (c0 >= n_valid) break;
+                    const bool in = i < n_valid;
+                    const float w = i < n ? s_w[i] : nerve_expf(v / T - m);
+                    s_w[i] = in ? w : 0.0f;
+                    float wv[64];
+                    static_for<0, 64>([&](auto J) __attribute__((always_inline)) { wv[J] = s_w[c0 + (uint32_t)J]; });
+                    float acc = carry;
+                    static_for<0, 64>([&](auto J) __attribute__((always_inline)) {
+                        acc = acc + ((uint32_t)J <= lane ? wv[J] : 0.0f);
+                    });
+                    s_p[i] = acc;
+                    carry = u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(min(64u, n_valid - c0) - 1u)));
                 }
-            }
-            if (nucleus == 0u) nucleus = 1u;
-            const float nucleus_weight = n_valid ? s_p[nucleus - 1u] : 0.0f;
-            PHASE_MARK(15);
-            const float target = u * nucleus_weight;
-            uint32_t selected = nucleus - 1u;
-            for (uint32_t c0 = 0; c0 < nucleus && c0 < n_valid; c0 += 64u) {
-                const uint32_t i = c0 + lane;
-                const uint64_t b = __ballot(i < nucleus && i < n_valid && target < s_p[i]);
-                if (b) {
-                    selected = c0 + (uint32_t)__builtin_ctzll(b);
-                    break;
+                const float total = n_valid ? carry : 0.0f;
+                const float threshold = P.top_p * total;
+                nucleus = n_valid;
+                for (uint32_t c0 = 0; c0 < n_valid; c0 += 64u) {
+                    const uint32_t i = c0 + lane;
+                    const uint64_t b = __ballot(i < n_valid && s_p[i] >= threshold);
+                    if (b) {
+                        nucleus = c0 + (uint32_t)__builtin_ctzll(b) + 1u;
+                        break;
+                    }
                 }
+                if (nucleus == 0u) nucleus = 1u;
+                nucleus_weight = n_valid ? s_p[nucleus - 1u] : 0.0f;
+                const float target = u * nucleus_weight;
+                selected = nucleus - 1u;
+                for (uint32_t c0 = 0; c0 < nucleus && c0 < n_valid; c0 += 64u) {
+                    const uint32_t i = c0 + lane;
+                    const uint64_t b = __ballot(i < nucleus && i < n_valid && target < s_p[i]);
+                    if (b) {
+                        selected = c0 + (uint32_t)__builtin_ctzll(b);
+                        break;
+                    }
+                }
+                for (uint32_t i = lane; i < k; i += 64u)
+                    s_p[i] = (i < nucleus && i < n_valid) ? s_w[i] / nucleus_weight : 0.0f;
             }
-            for (uint32_t i = lane; i < k; i += 64u) s_p[i] = (i < nucleus && i < n_valid) ? s_w[i] / nucleus_weight : 0.0f;
             if (lane == 0) {
                 const uint2 e = s_sorted[selected];
                 s_res[0] = e.y == kPadId ? kPadId : (e.y & kIdMask);
@@ -856,16 +890,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     const uint32_t row = logical / a.slices;
     const uint32_t slice = logical % a.slices;
 
-    const nerve_sampler_row_params P = a.params[row];
-    const RowIo io = a.slices == 1u ? load_row_io(a, row) : RowIo{0u, 0u, 0u, 0u};
-    const bool sampled = P.method != NERVE_METHOD_GREEDY;
-    uint32_t k = sampled ? P.top_k : 1u;
-    k = k < 1u ? 1u : (k > a.kcap ? a.kcap : k);
-    const uint32_t valid_min = sampled ? kMinFiniteKey : kNegInfKey;
-    const uint32_t masked_key = sampled ? 0u : kNegInfKey;
-    constexpr bool mask = MASK;  // an allowed-token bitmask is present
-    const bool lowering = P.repetition_penalty >= 1.0f && P.frequency_penalty >= 0.0f && P.presence_penalty >= 0.0f;
-
     const uint32_t nfull = a.nvec;
     const uint32_t v0 = min(slice * a.vec_per_slice, nfull);
     const uint32_t v1 = min(v0 + a.vec_per_slice, nfull);
@@ -878,21 +902,50 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     const bool has_tail = last_slice && tail_id < a.vocab;
 
     const Elem *lrow = (const Elem *)a.logits + (uint64_t)row * a.ld;
-    const uint32_t *arow = mask ? a.allowed + (uint64_t)row * a.allowed_stride : nullptr;
-    const uint32_t *srow = PEN == 1 ? a.seen + (uint64_t)row * a.seen_stride : nullptr;
 
     PHASE_MARK(0);
-    // 1. loads: history ids and bitmap words first (they are needed first),
-    // then the first D lane-vectors through a buffer resource bounded by v1
-    // (a slot past the slice reads as zero and is never used). A wave owns
-    // 64 * NV consecutive slots, so the loads of a lane sit 64 slots apart and
-    // share one offset register per 4 KiB.
+    // 1. loads: the first D lane-vectors first (they depend on the launch
+    // arguments only), through a buffer resource bounded by the wave's valid
+    // run; then the row parameters, history ids and bitmap words. A wave owns
+    // a run of consecutive slots, so the loads of a lane sit 64 slots apart
+    // and share one offset register per 4 KiB.
     const uint32_t lane = lane_id();
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // the slice is spread evenly: wave w owns `span` slots from w * span
     const uint32_t span = ((a.vec_per_slice + (uint32_t)kBlock - 1u) / (uint32_t)kBlock) * 64u;
     const uint32_t wslots = v1 - v0 > wave * span ? min(span, v1 - v0 - wave * span) : 0u;  // valid slots of the wave
     const uint32_t wbase = wave * span + lane;  // slot of lane-vector 0, relative to v0
+    // per-wave buffer resource: a load past the wave's valid run reads zero
+    // and costs no memory traffic
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(lrow + (uint64_t)(v0 + wave * span) * EPV), (short)0, (int)(wslots * kVecBytes), 0x00020000);
+    vec_t data[NV];
+    auto load = [&](int j) __attribute__((always_inline)) {
+        const uint32_t off = (lane + (uint32_t)j * 64u) * kVecBytes;
+        if constexpr (kVecBytes == 16) data[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
+        else if constexpr (kVecBytes == 4) data[j] = u2f(__builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, 0));
+        else data[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
+    };
+    // lane-vectors in flight ahead of the one being processed
+#ifndef NERVE_LOOKAHEAD
+#define NERVE_LOOKAHEAD 6
+#endif
+    constexpr int D = NV < NERVE_LOOKAHEAD ? NV : NERVE_LOOKAHEAD;
+    static_for<0, D>([&](auto J) __attribute__((always_inline)) { load(J); });
+
+    const nerve_sampler_row_params P = a.params[row];
+    const RowIo io = a.slices == 1u ? load_row_io(a, row) : RowIo{0u, 0u, 0u, 0u};
+    const bool sampled = P.method != NERVE_METHOD_GREEDY;
+    uint32_t k = sampled ? P.top_k : 1u;
+    k = k < 1u ? 1u : (k > a.kcap ? a.kcap : k);
+    const uint32_t valid_min = sampled ? kMinFiniteKey : kNegInfKey;
+    const uint32_t masked_key = sampled ? 0u : kNegInfKey;
+    constexpr bool mask = MASK;  // an allowed-token bitmask is present
+    const bool lowering = P.repetition_penalty >= 1.0f && P.frequency_penalty >= 0.0f && P.presence_penalty >= 0.0f;
+
+    const uint32_t *arow = mask ? a.allowed + (uint64_t)row * a.allowed_stride : nullptr;
+    const uint32_t *srow = PEN == 1 ? a.seen + (uint64_t)row * a.seen_stride : nullptr;
+
     uint32_t hist[history ? HPT : 1];
     uint32_t hlen = 0;
     if constexpr (history) {
@@ -913,23 +966,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
 #pragma unroll
         for (int i = 0; i < BW; ++i) sw[i] = srow[(bm_base >> 5) + min(tid + (uint32_t)i * kBlock, bm_last)];
     }
-    // per-wave buffer resource: a load past the wave's valid run reads zero
-    // and costs no memory traffic
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(lrow + (uint64_t)(v0 + wave * span) * EPV), (short)0, (int)(wslots * kVecBytes), 0x00020000);
-    vec_t data[NV];
-    auto load = [&](int j) __attribute__((always_inline)) {
-        const uint32_t off = (lane + (uint32_t)j * 64u) * kVecBytes;
-        if constexpr (kVecBytes == 16) data[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
-        else if constexpr (kVecBytes == 4) data[j] = u2f(__builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, 0));
-        else data[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
-    };
-    // lane-vectors in flight ahead of the one being processed
-#ifndef NERVE_LOOKAHEAD
-#define NERVE_LOOKAHEAD 6
-#endif
-    constexpr int D = NV < NERVE_LOOKAHEAD ? NV : NERVE_LOOKAHEAD;
-    static_for<0, D>([&](auto J) __attribute__((always_inline)) { load(J); });
     PHASE_MARK(1);
 
     // 2. LDS state: counters, mask / seen words of the slice (bits outside
@@ -1227,9 +1263,19 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             const uint32_t key = elem_key(tail_bits, tail_id);
             if (key >= thr && key != 0u) push(key, tail_id);
         }
+        // A raw key below thr cannot qualify (the configured value of a
+        // token in the vector passes never exceeds its raw value), so the
+        // bitmap and table lookups run only for raw keys >= thr. Masked
+        // tokens of greedy rows count as -inf, which only a threshold at or
+        // below -inf admits: then every element is examined.
+        const bool prefilter = thr > kNegInfKey;
         for (uint32_t q = tid; q < (nstaged << kLog2Epv); q += kBlock) {
-            const uint32_t key = staged_key(q);
-            if (key >= thr && key != 0u) push(key, s_sslot[q >> kLog2Epv] * EPV + (q & (uint32_t)(EPV - 1)));
+            const uint32_t i = q >> kLog2Epv, e = q & (uint32_t)(EPV - 1);
+            const uint32_t bits = VT::staged_bits(s_svec, i, e);
+            if (prefilter && raw_order_key(bits) < thr) continue;
+            const uint32_t id = s_sslot[i] * EPV + e;
+            const uint32_t key = elem_key(bits, id);
+            if (key >= thr && key != 0u) push(key, id);
         }
     };
     if (nstaged > kStageCap) {
