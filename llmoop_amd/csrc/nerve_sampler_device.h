@@ -1085,15 +1085,16 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         if constexpr (MASK) flags_group(std::true_type{}, J0);
     };
     uint32_t acc0 = VT::kAccInit, acc1 = VT::kAccInit;
+    // vmx[j]: the raw signed-integer maximum of lane-vector j, computed once
+    // by pass 1 and reused by pass 2
+    uint32_t vmx[NV];
     auto pass1 = [&](int j) __attribute__((always_inline)) {
+        vmx[j] = VT::vmax(data[j]);
         // branch-free: a lane-vector that is not ok contributes the empty marker
         const uint32_t sel = 0u - ((okm[j >> 5] >> (j & 31)) & 1u);
-        const uint32_t vm = (VT::vmax(data[j]) & sel) | (VT::kAccInit & ~sel);
+        const uint32_t vm = (vmx[j] & sel) | (VT::kAccInit & ~sel);
         if (j & 1) acc1 = VT::merge(acc1, vm);
         else acc0 = VT::merge(acc0, vm);
-        // pass 2 recomputes the maximum: keeping this one alive until then
-        // would cost a VGPR per lane-vector
-        asm volatile("" : "+v"(data[j]));
     };
     // Threshold from the reports. A lane reports the largest key among its
     // accumulated elements (itself an element of the slice). Every wave finds
@@ -1151,7 +1152,10 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         if (!sampled) has_nan |= ((uint32_t)j < nval && VT::has_nan(data[j])) ? 1u : 0u;
         bool go;
         if constexpr (FAST) {
-            go = ((live[j >> 5] >> (j & 31)) & 1u) && VT::ge_pos(VT::vmax(data[j]), thr);
+            // thr > +0: a slot past the run (loaded as zero) never passes, so
+            // without a mask the live flag adds nothing
+            const bool lv = !MASK || ((live[j >> 5] >> (j & 31)) & 1u);
+            go = lv && VT::ge_pos(vmx[j], thr);
         } else {
             const bool lv = skip_dead ? ((live[j >> 5] >> (j & 31)) & 1u) : ((uint32_t)j < nval);
             go = lv && VT::upper(data[j]) >= thr;
@@ -1163,7 +1167,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
                 s_sslot[pos] = v0 + wbase + (uint32_t)j * 64u;
             }
         }
-        asm volatile("" : "+v"(data[j]));  // as in pass 1: no maximum kept alive
     };
     constexpr int NA = NV / 2;
     static_assert(NV % 8 == 0, "lane-vector count must be a multiple of 8");
@@ -1209,7 +1212,10 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             static_for<0, NV / CH>([&](auto C) __attribute__((always_inline)) {
                 constexpr int j0 = C * CH, j1 = j0 + CH;
                 static_for<j0, j1>([&](auto J) __attribute__((always_inline)) { load(J); });
-                static_for<j0, j1>([&](auto J) __attribute__((always_inline)) { pass2(fast_tag, J); });
+                static_for<j0, j1>([&](auto J) __attribute__((always_inline)) {
+                    vmx[J] = VT::vmax(data[J]);
+                    pass2(fast_tag, J);
+                });
             });
         };
         if (fast) restage(std::true_type{});
