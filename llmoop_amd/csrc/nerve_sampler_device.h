@@ -550,6 +550,7 @@ struct SharedSmall {
     uint32_t ucount[2][kWaves];
     uint32_t uthr[2];
     uint32_t maxkey;
+    float u;  // the row's uniform draw
 };
 
 __device__ __forceinline__ uint32_t xcd_remap(uint32_t b, uint32_t n) {
@@ -594,7 +595,7 @@ __device__ __forceinline__ RowIo load_row_io(const StepArgs &a, uint32_t row) {
 template <typename Elem, int PEN, int NT>
 __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, const RowIo &io, const nerve_sampler_row_params &P, uint32_t k,
                            bool sampled, uint32_t n, uint32_t row_flags, uint2 *s_sorted, uint2 *s_big,
-                           float *s_w, float *s_p, uint32_t *s_hash, const RowCtx &ctx) {
+                           float *s_w, float *s_p, uint32_t *s_hash, const RowCtx &ctx, float u) {
     // s_w [kcap + 64]: the weights of s_sorted[0 .. n), written by the caller
     // (the rest are computed here), then zero past the min-p cut.
     // s_p [kcap]: running sums, then probabilities.
@@ -667,9 +668,6 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
         if (tid < 64) {
             const uint32_t lane = tid;
             const float T = P.temperature;
-            // the uniform draw does not depend on the weights: start it first
-            const uint64_t tick = (uint64_t)io.tick_lo | ((uint64_t)io.tick_hi << 32);
-            const float u = random_unit(a.rng, io.seed, tick, row);
             const float l0 = entry_value(s_sorted[0]);
             const float m = l0 / T;
             float minimum = u2f(kLowestBits);
@@ -689,23 +687,18 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
             if (k <= 64u) {
                 // one survivor per lane: values, weights and sums in registers
                 const bool live = lane < k;
-                const float v = live ? entry_value(s_sorted[lane]) : 0.0f;
+                const uint2 ev = live ? s_sorted[lane] : make_uint2(0u, 0u);
+                const float v = live ? entry_value(ev) : 0.0f;
                 const uint64_t below = __ballot(live && v < minimum);
                 if (below) n_valid = (uint32_t)__builtin_ctzll(below);
                 float w = 0.0f;
-                if (live) {
-                    if (lane < n) {
-                        w = s_w[lane];
-                    } else {
-                        w = nerve_expf(v / T - m);  // padding entries
-                        s_w[lane] = w;
-                    }
-                }
+                if (live) w = lane < n ? s_w[lane] : nerve_expf(v / T - m);  // padding entries computed here
+                s_w[lane] = lane < n_valid ? w : 0.0f;  // zero past the cut
                 float wv[64];
                 static_for<0, 64>([&](auto J) __attribute__((always_inline)) { wv[J] = s_w[(uint32_t)J]; });
                 float acc = 0.0f;
                 static_for<0, 64>([&](auto J) __attribute__((always_inline)) {
-                    if ((uint32_t)J < n_valid) acc = acc + ((uint32_t)J <= lane ? wv[J] : 0.0f);
+                    acc = acc + ((uint32_t)J <= lane ? wv[J] : 0.0f);
                 });
                 PHASE_MARK(10);
                 const float total = n_valid ? u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(n_valid - 1u))) : 0.0f;
@@ -718,7 +711,14 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
                 const float target = u * nucleus_weight;
                 const uint64_t bs = __ballot(lane < nucleus && lane < n_valid && target < acc);
                 selected = bs ? (uint32_t)__builtin_ctzll(bs) : nucleus - 1u;
-                if (live) s_p[lane] = (lane < nucleus && lane < n_valid) ? w / nucleus_weight : 0.0f;
+                if (a.topk_probs && live) s_p[lane] = (lane < nucleus && lane < n_valid) ? w / nucleus_weight : 0.0f;
+                // the selected survivor is in lane `selected`
+                const uint32_t sid = __builtin_amdgcn_readlane(ev.y, (int)selected);
+                const uint32_t sbits = __builtin_amdgcn_readlane(f2u(v), (int)selected);
+                if (lane == 0) {
+                    s_res[0] = sid == kPadId ? kPadId : (sid & kIdMask);
+                    s_res[1] = sbits;
+                }
             } else {
                 // chunks of 64 survivors; s_w is zeroed past the cut
                 float carry = 0.0f;  // P_(c0 - 1)
@@ -765,11 +765,11 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
                 }
                 for (uint32_t i = lane; i < k; i += 64u)
                     s_p[i] = (i < nucleus && i < n_valid) ? s_w[i] / nucleus_weight : 0.0f;
-            }
-            if (lane == 0) {
-                const uint2 e = s_sorted[selected];
-                s_res[0] = e.y == kPadId ? kPadId : (e.y & kIdMask);
-                s_res[1] = f2u(entry_value(e));
+                if (lane == 0) {
+                    const uint2 e = s_sorted[selected];
+                    s_res[0] = e.y == kPadId ? kPadId : (e.y & kIdMask);
+                    s_res[1] = f2u(entry_value(e));
+                }
             }
         }
         __syncthreads();
@@ -1007,6 +1007,12 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         }
     }
     lds_sync();
+    // the uniform draw depends only on the seed and tick: one wave computes it
+    // now, off the finish's critical path
+    if (sampled && a.slices == 1u && wave == 1u) {
+        const float uu = random_unit(a.rng, io.seed, (uint64_t)io.tick_lo | ((uint64_t)io.tick_hi << 32), row);
+        if (lane == 0u) sm.u = uu;
+    }
     // The penalty state (seen words, or history ids -> bitmap + repeat table)
     // is needed only by the exact pass after the stream, so it is built at the
     // midpoint of the stream, when its loads have long landed.
@@ -1480,7 +1486,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     }
     const RowIo io_l = {sm.io[0], sm.io[1], sm.io[2], sm.io[3]};
     finish_row<Elem, PEN, kBlock>(a, row, io_l, P, k, sampled, n_out, flags_slice, s_sorted, s_big, s_wt,
-                                  (float *)s_big + 64, s_hash, ctx);
+                                  (float *)s_big + 64, s_hash, ctx, sm.u);
     PHASE_MARK(12);
 }
 
@@ -1501,6 +1507,7 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
     const bool sampled = P.method != NERVE_METHOD_GREEDY;
     uint32_t k = sampled ? P.top_k : 1u;
     k = k < 1u ? 1u : (k > a.kcap ? a.kcap : k);
+    const float u = sampled ? random_unit(a.rng, io.seed, (uint64_t)io.tick_lo | ((uint64_t)io.tick_hi << 32), row) : 0.0f;
 
     const uint2 *all = a.scratch_lists + (uint64_t)row * a.slices * a.kcap;
     const uint32_t *meta = a.scratch_meta + row * a.slices;
@@ -1557,7 +1564,7 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
     ctx.pres = P.presence_penalty;
     ctx.history = PEN == 2;
     finish_row<Elem, PEN, kFinishBlock>(a, row, io, P, k, sampled, n, row_flags, s_sorted, s_big, s_wt, (float *)s_big,
-                                        s_hash, ctx);
+                                        s_hash, ctx, u);
 }
 
 // ---- launch ------------------------------------------------------------------
