@@ -974,7 +974,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     if constexpr (history) {
         const uint4 empty4 = make_uint4(kHashEmpty, kHashEmpty, kHashEmpty, kHashEmpty);
         for (uint32_t i = tid; i < a.hash_slots / 4u; i += kBlock) ((uint4 *)s_hash)[i] = empty4;
-        for (uint32_t i = tid; i < bm_n; i += kBlock) s_pen[i] = 0u;
+        for (uint32_t i = tid; i < bm_n; i += kBlock) s_pen[i] = 0u;  // (bm_n need not be a multiple of 4)
     }
     if (tid == 0) {
         sm.flag[1] = 0u;  // candidates
@@ -1024,20 +1024,17 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
                 if (w < bm_n) s_pen[w] = sw[i] & range_bits(w);
             }
         }
+    };
+    // history id h of this lane -> bitmap; a repeat (its bit already set) ->
+    // the table of occurrences beyond the first. One id per second-half step,
+    // so the LDS round trips overlap the loads in flight.
+    auto insert_history = [&](int h) __attribute__((always_inline)) {
         if constexpr (history) {
-            uint32_t first[HPT];
-#pragma unroll
-            for (int h = 0; h < HPT; ++h) {
-                const uint32_t id = hist[h];
-                first[h] = 0xffffffffu;
-                if (tid + (uint32_t)h * kBlock < hlen && id >= tok0 && id < tok1) {
-                    const uint32_t o = id - bm_base;
-                    first[h] = atomicOr(&s_pen[o >> 5], 1u << (o & 31u)) & (1u << (o & 31u));
-                }
+            const uint32_t id = hist[h];
+            if (tid + (uint32_t)h * kBlock < hlen && id >= tok0 && id < tok1) {
+                const uint32_t o = id - bm_base, bit = 1u << (o & 31u);
+                if (atomicOr(&s_pen[o >> 5], bit) & bit) hash_insert(s_hash, a.log2_slots, id);
             }
-#pragma unroll
-            for (int h = 0; h < HPT; ++h)
-                if (first[h] != 0xffffffffu && first[h] != 0u) hash_insert(s_hash, a.log2_slots, hist[h]);
         }
     };
     PHASE_MARK(2);
@@ -1191,10 +1188,15 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             step_in(J);
             pass2(fast_tag, J - NA);
             pass2(fast_tag, J);
+            if constexpr (J - NA < HPT) insert_history(J - NA);
         });
     };
     if (fast) second_half(std::true_type{});
     else second_half(std::false_type{});
+    if constexpr (history && NV - NA < HPT) {
+        // history ids left over when the second half has fewer steps
+        static_for<NV - NA, HPT>([&](auto H) __attribute__((always_inline)) { insert_history(H); });
+    }
     // the V % EPV tail of the last slice, one element per lane (loaded late:
     // it is rare and holding it across the stream costs a VGPR)
     const uint32_t tail_bits = has_tail ? f2u(load_elem<Elem>(lrow, tail_id)) : 0u;
