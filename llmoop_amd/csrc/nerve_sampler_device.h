@@ -66,6 +66,7 @@ constexpr int kBlock = 512;
 constexpr int kWaves = kBlock / 64;
 constexpr int kFinishBlock = 256;
 constexpr uint32_t kCandCap = 1024;
+constexpr uint32_t kRankPad = 128;  // candidate counts the unrolled rank sort handles
 constexpr uint32_t kHashEmpty = 0xffffffffu;
 constexpr uint32_t kMaxHistory = NERVE_MAX_HISTORY_CAPACITY;
 
@@ -592,6 +593,25 @@ __device__ __forceinline__ RowIo load_row_io(const StepArgs &a, uint32_t row) {
 // Writes the output record, optional survivors / probabilities, the stream
 // control tick and the output ring. Runs on NT threads; wave 0 does the
 // sequential running sums.
+// Running sums of one wave's lane values in sequential order: lane l gets
+// (((c + w_0) + w_1) + ... + w_l), rounded after every add exactly as a
+// sequential loop rounds. Each step adds a lane's own value to the sum of its
+// left neighbour (a wavefront shift by one lane; lane 0 reads c), so the sum
+// of lane l is final after l steps and unchanged by later ones. Lanes at or
+// past `len` hold partial sums.
+__device__ __forceinline__ float sequential_prefix(float w, float c, uint32_t len) {
+    float acc = c + w;
+    // steps in groups of 8 (steps past len - 1 change no final sum)
+    for (uint32_t step = 1; step < len; step += 8u) {
+        static_for<0, 8>([&](auto) __attribute__((always_inline)) {
+            // dpp_ctrl 0x138: wave_shr:1 (lane l reads lane l - 1; lane 0 keeps `old`)
+            const float left = u2f((uint32_t)__builtin_amdgcn_update_dpp((int)f2u(c), (int)f2u(acc), 0x138, 0xf, 0xf, false));
+            acc = left + w;
+        });
+    }
+    return acc;
+}
+
 template <typename Elem, int PEN, int NT>
 __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, const RowIo &io, const nerve_sampler_row_params &P, uint32_t k,
                            bool sampled, uint32_t n, uint32_t row_flags, uint2 *s_sorted, uint2 *s_big,
@@ -599,7 +619,6 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
     // s_w [kcap + 64]: the weights of s_sorted[0 .. n), written by the caller
     // (the rest are computed here), then zero past the min-p cut.
     // s_p [kcap]: running sums, then probabilities.
-    __shared__ uint32_t s_res[2];
     const uint32_t tid = threadIdx.x;
     uint32_t token = 0, sel_bits = 0, out_flags = 0, kout = 1;
     uint32_t *sc = a.stream_control ? a.stream_control + (uint64_t)row * 5u : nullptr;
@@ -660,126 +679,106 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
                 sel_bits = f2u(entry_value(e));
             }
         }
-        __syncthreads();
         if (tid == 0) s_p[0] = 1.0f;
-    } else {
-        for (uint32_t i = n + tid; i < k; i += NT) s_sorted[i] = make_uint2(kMinFiniteKey, kPadId);
-        __syncthreads();
-        if (tid < 64) {
-            const uint32_t lane = tid;
-            const float T = P.temperature;
-            const float l0 = entry_value(s_sorted[0]);
-            const float m = l0 / T;
-            float minimum = u2f(kLowestBits);
-            if (P.min_p > 0.0f) {
-                const float lg = nerve_logf(P.min_p);
-                const float d = T * lg;
-                minimum = l0 + d;
-            }
-            PHASE_MARK(13);
-            // The min-p cut (the first survivor below the floor ends the
-            // list), then running sums in the reference's sequential order:
-            // lane i adds w_0, w_1, ... in turn and +0.0 (exact) for the terms
-            // after its own, so its sum is the reference's prefix sum P_i,
-            // rounding for rounding.
-            uint32_t n_valid = k, nucleus, selected;
-            float nucleus_weight;
-            if (k <= 64u) {
-                // one survivor per lane: values, weights and sums in registers
-                const bool live = lane < k;
-                const uint2 ev = live ? s_sorted[lane] : make_uint2(0u, 0u);
-                const float v = live ? entry_value(ev) : 0.0f;
-                const uint64_t below = __ballot(live && v < minimum);
-                if (below) n_valid = (uint32_t)__builtin_ctzll(below);
-                float w = 0.0f;
-                if (live) w = lane < n ? s_w[lane] : nerve_expf(v / T - m);  // padding entries computed here
-                s_w[lane] = lane < n_valid ? w : 0.0f;  // zero past the cut
-                float wv[64];
-                static_for<0, 64>([&](auto J) __attribute__((always_inline)) { wv[J] = s_w[(uint32_t)J]; });
-                float acc = 0.0f;
-                static_for<0, 64>([&](auto J) __attribute__((always_inline)) {
-                    acc = acc + ((uint32_t)J <= lane ? wv[J] : 0.0f);
-                });
-                PHASE_MARK(10);
-                const float total = n_valid ? u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(n_valid - 1u))) : 0.0f;
-                const float threshold = P.top_p * total;
-                const uint64_t bn = __ballot(lane < n_valid && acc >= threshold);
-                nucleus = bn ? (uint32_t)__builtin_ctzll(bn) + 1u : n_valid;
-                if (nucleus == 0u) nucleus = 1u;
-                nucleus_weight = n_valid ? u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(nucleus - 1u))) : 0.0f;
-                PHASE_MARK(15);
-                const float target = u * nucleus_weight;
-                const uint64_t bs = __ballot(lane < nucleus && lane < n_valid && target < acc);
-                selected = bs ? (uint32_t)__builtin_ctzll(bs) : nucleus - 1u;
-                if (a.topk_probs && live) s_p[lane] = (lane < nucleus && lane < n_valid) ? w / nucleus_weight : 0.0f;
-                // the selected survivor is in lane `selected`
-                const uint32_t sid = __builtin_amdgcn_readlane(ev.y, (int)selected);
-                const uint32_t sbits = __builtin_amdgcn_readlane(f2u(v), (int)selected);
-                if (lane == 0) {
-                    s_res[0] = sid == kPadId ? kPadId : (sid & kIdMask);
-                    s_res[1] = sbits;
-                }
-            } else {
-                // chunks of 64 survivors; s_w is zeroed past the cut
-                float carry = 0.0f;  // P_(c0 - 1)
-                for (uint32_t c0 = 0; c0 < n_valid; c0 += 64u) {
-                    const uint32_t i = c0 + lane;
-                    const float v = i < k ? entry_value(s_sorted[i]) : 0.0f;
-                    const uint64_t below = __ballot(i < k && v < minimum);
-                    if (below) n_valid = min(n_valid, c0 + (uint32_t)__builtin_ctzll(below));
-                    if (c0 >= n_valid) break;
-                    const bool in = i < n_valid;
-                    const float w = i < n ? s_w[i] : nerve_expf(v / T - m);
-                    s_w[i] = in ? w : 0.0f;
-                    float wv[64];
-                    static_for<0, 64>([&](auto J) __attribute__((always_inline)) { wv[J] = s_w[c0 + (uint32_t)J]; });
-                    float acc = carry;
-                    static_for<0, 64>([&](auto J) __attribute__((always_inline)) {
-                        acc = acc + ((uint32_t)J <= lane ? wv[J] : 0.0f);
-                    });
-                    s_p[i] = acc;
-                    carry = u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(min(64u, n_valid - c0) - 1u)));
-                }
-                const float total = n_valid ? carry : 0.0f;
-                const float threshold = P.top_p * total;
-                nucleus = n_valid;
-                for (uint32_t c0 = 0; c0 < n_valid; c0 += 64u) {
-                    const uint32_t i = c0 + lane;
-                    const uint64_t b = __ballot(i < n_valid && s_p[i] >= threshold);
-                    if (b) {
-                        nucleus = c0 + (uint32_t)__builtin_ctzll(b) + 1u;
-                        break;
-                    }
-                }
-                if (nucleus == 0u) nucleus = 1u;
-                nucleus_weight = n_valid ? s_p[nucleus - 1u] : 0.0f;
-                const float target = u * nucleus_weight;
-                selected = nucleus - 1u;
-                for (uint32_t c0 = 0; c0 < nucleus && c0 < n_valid; c0 += 64u) {
-                    const uint32_t i = c0 + lane;
-                    const uint64_t b = __ballot(i < nucleus && i < n_valid && target < s_p[i]);
-                    if (b) {
-                        selected = c0 + (uint32_t)__builtin_ctzll(b);
-                        break;
-                    }
-                }
-                for (uint32_t i = lane; i < k; i += 64u)
-                    s_p[i] = (i < nucleus && i < n_valid) ? s_w[i] / nucleus_weight : 0.0f;
-                if (lane == 0) {
-                    const uint2 e = s_sorted[selected];
-                    s_res[0] = e.y == kPadId ? kPadId : (e.y & kIdMask);
-                    s_res[1] = f2u(entry_value(e));
-                }
-            }
+    } else if (tid < 64) {
+        // Sampled rows: wave 0 finishes alone (no block barriers). Entries
+        // past the n candidates are padding (the lowest finite value, an
+        // invalid id).
+        const uint32_t lane = tid;
+        const uint2 pad = make_uint2(kMinFiniteKey, kPadId);
+        const float T = P.temperature;
+        const float l0 = entry_value(n ? s_sorted[0] : pad);
+        const float m = l0 / T;
+        float minimum = u2f(kLowestBits);
+        if (P.min_p > 0.0f) {
+            const float lg = nerve_logf(P.min_p);
+            const float d = T * lg;
+            minimum = l0 + d;
         }
-        __syncthreads();
+        PHASE_MARK(13);
+        // The min-p cut (the first survivor below the floor ends the list),
+        // then running sums in the reference's sequential order.
+        uint32_t n_valid = k, nucleus, selected;
+        float nucleus_weight;
+        if (k <= 64u) {
+            // one survivor per lane: values, weights and sums in registers
+            const bool live = lane < k;
+            const uint2 ev = lane < n ? s_sorted[lane] : pad;
+            const float v = live ? entry_value(ev) : 0.0f;
+            const uint64_t below = __ballot(live && v < minimum);
+            if (below) n_valid = (uint32_t)__builtin_ctzll(below);
+            float w = 0.0f;
+            if (lane < n_valid) w = lane < n ? s_w[lane] : nerve_expf(v / T - m);  // padding entries computed here
+            const float acc = sequential_prefix(w, 0.0f, n_valid);
+            PHASE_MARK(10);
+            const float total = n_valid ? u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(n_valid - 1u))) : 0.0f;
+            const float threshold = P.top_p * total;
+            const uint64_t bn = __ballot(lane < n_valid && acc >= threshold);
+            nucleus = bn ? (uint32_t)__builtin_ctzll(bn) + 1u : n_valid;
+            if (nucleus == 0u) nucleus = 1u;
+            nucleus_weight = n_valid ? u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(nucleus - 1u))) : 0.0f;
+            PHASE_MARK(15);
+            const float target = u * nucleus_weight;
+            const uint64_t bs = __ballot(lane < nucleus && lane < n_valid && target < acc);
+            selected = bs ? (uint32_t)__builtin_ctzll(bs) : nucleus - 1u;
+            if (a.topk_probs && live) s_p[lane] = (lane < nucleus && lane < n_valid) ? w / nucleus_weight : 0.0f;
+            // the selected survivor is in lane `selected`
+            const uint32_t sid = __builtin_amdgcn_readlane(ev.y, (int)selected);
+            token = sid == kPadId ? kPadId : (sid & kIdMask);
+            sel_bits = __builtin_amdgcn_readlane(f2u(v), (int)selected);
+        } else {
+            // chunks of 64 survivors: s_w holds the weights (zero past the
+            // cut), s_p the running sums
+            for (uint32_t i = n + lane; i < k; i += 64u) s_sorted[i] = pad;
+            float carry = 0.0f;  // P_(c0 - 1)
+            for (uint32_t c0 = 0; c0 < n_valid; c0 += 64u) {
+                const uint32_t i = c0 + lane;
+                const float v = i < k ? entry_value(s_sorted[i]) : 0.0f;
+                const uint64_t below = __ballot(i < k && v < minimum);
+                if (below) n_valid = min(n_valid, c0 + (uint32_t)__builtin_ctzll(below));
+                if (c0 >= n_valid) break;
+                const bool in = i < n_valid;
+                float w = 0.0f;
+                if (in) w = i < n ? s_w[i] : nerve_expf(v / T - m);
+                if (i < k) s_w[i] = w;
+                const uint32_t len = min(64u, n_valid - c0);
+                const float acc = sequential_prefix(w, carry, len);
+                s_p[i] = acc;
+                carry = u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(len - 1u)));
+            }
+            const float total = n_valid ? carry : 0.0f;
+            const float threshold = P.top_p * total;
+            nucleus = n_valid;
+            for (uint32_t c0 = 0; c0 < n_valid; c0 += 64u) {
+                const uint32_t i = c0 + lane;
+                const uint64_t b = __ballot(i < n_valid && s_p[i] >= threshold);
+                if (b) {
+                    nucleus = c0 + (uint32_t)__builtin_ctzll(b) + 1u;
+                    break;
+                }
+            }
+            if (nucleus == 0u) nucleus = 1u;
+            nucleus_weight = n_valid ? s_p[nucleus - 1u] : 0.0f;
+            const float target = u * nucleus_weight;
+            selected = nucleus - 1u;
+            for (uint32_t c0 = 0; c0 < nucleus && c0 < n_valid; c0 += 64u) {
+                const uint32_t i = c0 + lane;
+                const uint64_t b = __ballot(i < nucleus && i < n_valid && target < s_p[i]);
+                if (b) {
+                    selected = c0 + (uint32_t)__builtin_ctzll(b);
+                    break;
+                }
+            }
+            for (uint32_t i = lane; i < k; i += 64u)
+                s_p[i] = (i < nucleus && i < n_valid) ? s_w[i] / nucleus_weight : 0.0f;
+            const uint2 e = s_sorted[selected];
+            token = e.y == kPadId ? kPadId : (e.y & kIdMask);
+            sel_bits = f2u(entry_value(e));
+        }
         PHASE_MARK(11);
-        token = s_res[0];
-        sel_bits = s_res[1];
         out_flags = NERVE_FLAG_SAMPLED;
         kout = k;
     }
-    __syncthreads();
 
     if (tid == 0) {
         nerve_sampler_output o;
@@ -808,6 +807,8 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
         }
     }
     if (a.topk_ids || a.topk_logits || a.topk_probs) {
+        if (sampled && !eos) kout = k;  // set by wave 0 only
+        __syncthreads();                // s_p is written by wave 0
         for (uint32_t i = tid; i < a.kcap; i += NT) {
             const uint64_t o = (uint64_t)row * a.kcap + i;
             const bool live = i < kout;
@@ -817,7 +818,7 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
                 value = eos ? u2f(kLowestBits) : u2f(sel_bits);
                 id = token;
             } else if (live) {
-                const uint2 e = s_sorted[i];
+                const uint2 e = i < n ? s_sorted[i] : make_uint2(kMinFiniteKey, kPadId);
                 value = entry_value(e);
                 id = e.y == kPadId ? kPadId : (e.y & kIdMask);
             }
@@ -976,6 +977,8 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         for (uint32_t i = tid; i < a.hash_slots / 4u; i += kBlock) ((uint4 *)s_hash)[i] = empty4;
         for (uint32_t i = tid; i < bm_n; i += kBlock) s_pen[i] = 0u;  // (bm_n need not be a multiple of 4)
     }
+    // the candidate list reads as zero past its end (the rank sort's padding)
+    if (tid < kRankPad) s_cand[tid] = make_uint2(0u, 0u);
     if (tid == 0) {
         sm.flag[1] = 0u;  // candidates
         sm.flag[2] = 0u;  // staged lane-vectors
@@ -1244,7 +1247,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     auto push = [&](uint32_t key, uint32_t id) __attribute__((always_inline)) {
         const uint32_t pos = atomicAdd(&sm.flag[1], 1u);
         if (pos < kStreamCandCap) s_cand[pos] = make_uint2(key, id);
-        atomicMax(&sm.maxkey, key);
     };
     auto count_of = [&](uint32_t id) __attribute__((always_inline)) -> uint32_t {
         return history ? 1u + hash_lookup(s_hash, a.log2_slots, id) : 1u;
@@ -1277,19 +1279,71 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             const uint32_t key = elem_key(tail_bits, tail_id);
             if (key >= thr && key != 0u) push(key, tail_id);
         }
-        // A raw key below thr cannot qualify (the configured value of a
-        // token in the vector passes never exceeds its raw value), so the
-        // bitmap and table lookups run only for raw keys >= thr. Masked
-        // tokens of greedy rows count as -inf, which only a threshold at or
-        // below -inf admits: then every element is examined.
-        const bool prefilter = thr > kNegInfKey;
-        for (uint32_t q = tid; q < (nstaged << kLog2Epv); q += kBlock) {
-            const uint32_t i = q >> kLog2Epv, e = q & (uint32_t)(EPV - 1);
-            const uint32_t bits = VT::staged_bits(s_svec, i, e);
-            if (prefilter && raw_order_key(bits) < thr) continue;
-            const uint32_t id = s_sslot[i] * EPV + e;
-            const uint32_t key = elem_key(bits, id);
-            if (key >= thr && key != 0u) push(key, id);
+        // One staged lane-vector per lane, spread over the waves (vector i
+        // to wave i % 8). A raw key below thr cannot qualify (the configured
+        // value of a token in the vector passes never exceeds its raw value),
+        // so only raw keys >= thr are examined further. Masked tokens of
+        // greedy rows count as -inf, which only a threshold at or below -inf
+        // admits: then every element is examined. The EPV ids of a
+        // lane-vector share one word of each bitmap; penalised ones (rare)
+        // take the table lookup. Appends are counted per wave: one LDS atomic
+        // per wave and round.
+        const uint32_t thr_raw = thr > kNegInfKey ? thr : 0u;  // the raw-key prefilter
+        constexpr uint32_t kElemMask = (1u << EPV) - 1u;
+        for (uint32_t base = 0; base < nstaged; base += kBlock) {
+            const uint32_t i = base + lane * (uint32_t)kWaves + wave;
+            const bool valid = i < nstaged;
+            const uint32_t ic = valid ? i : 0u;
+            const vec_t v = s_svec[ic];
+            const uint32_t id0 = s_sslot[ic] * EPV;
+            const uint32_t off = id0 - bm_base;
+            const uint32_t allow_bits = mask ? (s_allow[off >> 5] >> (off & 31u)) & kElemMask : kElemMask;
+            uint32_t pen_bits = 0u;
+            if constexpr (PEN != 0) pen_bits = (s_pen[off >> 5] >> (off & 31u)) & kElemMask;
+            // branch-free: the key of every element, zero where it cannot qualify
+            uint32_t keys[EPV];
+            uint32_t cand = 0u;
+            static_for<0, EPV>([&](auto E) __attribute__((always_inline)) {
+                constexpr uint32_t bit = 1u << (int)E;
+                const uint32_t raw = raw_order_key(VT::bits(v, E));
+                const bool c = valid && raw >= thr_raw;
+                cand |= c ? bit : 0u;
+                uint32_t key = (allow_bits & bit) ? raw : masked_key;
+                key = (c && !(pen_bits & bit)) ? key : 0u;
+                keys[E] = (key < valid_min || key < thr) ? 0u : key;
+            });
+            uint32_t pb = pen_bits & cand;
+            while (pb) {
+                // penalised candidates (rare): configured value from the count
+                const uint32_t e = (uint32_t)__builtin_ctz(pb);
+                pb &= pb - 1u;
+                uint32_t key = 0u;
+                if (lowering) {
+                    key = pen_key(VT::bits_dyn(v, e), ((allow_bits >> e) & 1u) != 0u, count_of(id0 + e));
+                    if (key < valid_min || key < thr) key = 0u;
+                }
+                static_for<0, EPV>([&](auto E) __attribute__((always_inline)) { keys[E] = e == (uint32_t)E ? key : keys[E]; });
+            }
+            uint32_t nq = 0u;
+            static_for<0, EPV>([&](auto E) __attribute__((always_inline)) { nq += keys[E] != 0u ? 1u : 0u; });
+            // exclusive prefix and total of nq over the wave, bit by bit
+            uint32_t excl = 0u, tot = 0u;
+            static_for<0, (EPV > 1 ? 4 : 1)>([&](auto B) __attribute__((always_inline)) {
+                const uint64_t m = __ballot((nq >> (int)B) & 1u);
+                excl += __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u)) << (int)B;
+                tot += (uint32_t)__builtin_popcountll(m) << (int)B;
+            });
+            if (tot) {
+                uint32_t pos0 = 0u;
+                if (lane == 0u) pos0 = atomicAdd(&sm.flag[1], tot);
+                uint32_t pos = (uint32_t)__builtin_amdgcn_readlane((int)pos0, 0) + excl;
+                static_for<0, EPV>([&](auto E) __attribute__((always_inline)) {
+                    if (keys[E] != 0u) {
+                        if (pos < kStreamCandCap) s_cand[pos] = make_uint2(keys[E], id0 + (uint32_t)E);
+                        ++pos;
+                    }
+                });
+            }
         }
     };
     if (nstaged > kStageCap) {
@@ -1314,6 +1368,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             }
         }
     }
+    PHASE_MARK(3);
     {
         // slice flags: bit 0 = some token allowed, bit 1 = greedy row holds a NaN
         const uint32_t f = (__ballot(any_allowed != 0u) ? 1u : 0u) | (__ballot(has_nan != 0u) ? 2u : 0u);
@@ -1321,7 +1376,9 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     }
     lds_sync();
     const uint32_t flags_slice = sm.flag[3];
+    bool repad = false;  // the candidate list was rewritten: its padding is stale
     if (nstaged <= kStageCap && sm.flag[1] > kStreamCandCap && (PEN == 0 || lowering)) {
+        repad = true;
         // Too many candidates for a weak threshold: the exact k-th key of the
         // staged elements (plus the tail) is a threshold that keeps at least k.
         lds_sync();
@@ -1372,6 +1429,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             const uint32_t key = order_key(configured_at<Elem>(ctx, tt));
             return key < valid_min ? 0u : key;
         };
+        repad = true;
         uint32_t count_ge;
         const uint32_t kv = radix_threshold_fn(tok0, tok1, k, sm.hist, sm.sel, count_ge, key_at);
         uint32_t gt = 0;
@@ -1388,7 +1446,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             if (key != 0u && (key > kv || (key == kv && need && tt <= id_cut))) {
                 const uint32_t q = atomicAdd(&sm.flag[1], 1u);
                 if (q < kStreamCandCap) s_cand[q] = make_uint2(key, tt);
-                atomicMax(&sm.maxkey, key);
             }
         }
         lds_sync();
@@ -1397,7 +1454,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     // Many candidates (a weak threshold): keep the entries at or above the
     // k-th largest key (LDS radix select) in the staging area, which is free
     // by now, so the rank sort below stays small.
-    const uint2 *list = s_cand;
+    uint2 *list = s_cand;
     constexpr uint32_t kTrimCap = kStageCap * (uint32_t)sizeof(vec_t) / 8u;
     if (C > 256u && C > 4u * k) {
         auto cand_key = [&](uint32_t i) __attribute__((always_inline)) -> uint32_t { return s_cand[i].x; };
@@ -1417,6 +1474,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         if (sm.flag[0] <= kTrimCap) {
             list = s_trim;
             C = sm.flag[0];
+            repad = true;
         }
     }
     // The writer of rank r also settles the sign of a zero survivor (from its
@@ -1425,32 +1483,82 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     // of a zero l cannot change a weight).
     float *s_wt = (float *)s_sslot;  // [kcap + 64], the staging slots are free by now
     const float T = P.temperature;
-    const float m_w = sampled ? key_to_float(sm.maxkey) / T : 0.0f;
-    auto emit = [&](uint32_t r, uint2 e) __attribute__((always_inline)) {
+    auto emit = [&](uint32_t r, uint2 e, uint32_t maxkey) __attribute__((always_inline)) {
         if (e.x == kZeroKey && f2u(configured_at<Elem>(ctx, e.y)) == 0x80000000u) e.y |= kNegZeroFlag;
         s_sorted[r] = e;
-        if (sampled && a.slices == 1u) s_wt[r] = nerve_expf(entry_value(e) / T - m_w);
+        if (sampled && a.slices == 1u) s_wt[r] = nerve_expf(entry_value(e) / T - key_to_float(maxkey) / T);
     };
     // rank sort (ids are distinct, so ranks are a permutation): G adjacent
     // lanes share a candidate, each counting the better entries in every G-th
     // position, and the partial ranks are summed across the group
-    if (C <= 128u) {
-        // the common case, unrolled: every comparison's read is issued at once
-        const uint32_t G = C <= 64u ? 8u : 4u;
-        const uint32_t i = tid / G, part = tid % G;
-        const uint2 e = i < C ? list[i] : make_uint2(0u, 0u);
-        // (key, ~id) as one unsigned 64-bit value orders like entry_better
-        const uint64_t pe = ((uint64_t)e.x << 32) | (uint64_t)(~e.y);
-        uint32_t r = 0;
-        uint2 o[32];
-        static_for<0, 32>([&](auto J) __attribute__((always_inline)) { o[J] = list[part + G * (uint32_t)J]; });
-        static_for<0, 32>([&](auto J) __attribute__((always_inline)) {
-            const uint64_t po = ((uint64_t)o[J].x << 32) | (uint64_t)(~o[J].y);
-            r += (part + G * (uint32_t)J < C && po > pe) ? 1u : 0u;
-        });
-        for (uint32_t off = 1u; off < G; off <<= 1) r += __shfl_xor(r, (int)off, 64);
-        if (i < C && part == 0u && r < k) emit(r, e);
+    PHASE_MARK(9);
+    if (C <= kRankPad) {
+        // The common case, unrolled: 8 adjacent lanes share a candidate (two,
+        // i and i + 64, past 64 candidates), each comparing it with every 8th
+        // list entry. (key, ~id) as one unsigned 64-bit value orders like
+        // entry_better; the list reads as (0, 0) past C, which ranks below
+        // every candidate (keys are nonzero).
+        if (repad) {
+            for (uint32_t i = C + tid; i < kRankPad; i += kBlock) list[i] = make_uint2(0u, 0u);
+            lds_sync();
+        }
+        auto packed = [](uint2 e) __attribute__((always_inline)) -> uint64_t {
+            return ((uint64_t)e.x << 32) | (uint64_t)(~e.y);
+        };
+        const uint32_t i = tid >> 3, part = tid & 7u;
+        const uint2 e0 = list[i];
+        const uint64_t p0 = packed(e0);
+        if (C <= 64u) {
+            uint2 o[8];
+            static_for<0, 8>([&](auto J) __attribute__((always_inline)) { o[J] = list[part + 8u * (uint32_t)J]; });
+            uint32_t r = 0, mx = 0;
+            static_for<0, 8>([&](auto J) __attribute__((always_inline)) {
+                r += packed(o[J]) > p0 ? 1u : 0u;
+                mx = max(mx, o[J].x);
+            });
+            // the 8 lanes of a group read the whole list: mx becomes its largest key
+            r += __shfl_xor(r, 1, 64);
+            mx = max(mx, (uint32_t)__shfl_xor((int)mx, 1, 64));
+            r += __shfl_xor(r, 2, 64);
+            mx = max(mx, (uint32_t)__shfl_xor((int)mx, 2, 64));
+            r += __shfl_xor(r, 4, 64);
+            mx = max(mx, (uint32_t)__shfl_xor((int)mx, 4, 64));
+            if (i < C && part == 0u && r < k) emit(r, e0, mx);
+        } else {
+            const uint2 e1 = list[i + 64u];
+            const uint64_t p1 = packed(e1);
+            uint2 o[16];
+            static_for<0, 16>([&](auto J) __attribute__((always_inline)) { o[J] = list[part + 8u * (uint32_t)J]; });
+            uint32_t r0 = 0, r1 = 0, mx = 0;
+            static_for<0, 16>([&](auto J) __attribute__((always_inline)) {
+                const uint64_t po = packed(o[J]);
+                r0 += po > p0 ? 1u : 0u;
+                r1 += po > p1 ? 1u : 0u;
+                mx = max(mx, o[J].x);
+            });
+            r0 += __shfl_xor(r0, 1, 64);
+            r1 += __shfl_xor(r1, 1, 64);
+            mx = max(mx, (uint32_t)__shfl_xor((int)mx, 1, 64));
+            r0 += __shfl_xor(r0, 2, 64);
+            r1 += __shfl_xor(r1, 2, 64);
+            mx = max(mx, (uint32_t)__shfl_xor((int)mx, 2, 64));
+            r0 += __shfl_xor(r0, 4, 64);
+            r1 += __shfl_xor(r1, 4, 64);
+            mx = max(mx, (uint32_t)__shfl_xor((int)mx, 4, 64));
+            if (part == 0u) {
+                if (i < C && r0 < k) emit(r0, e0, mx);
+                if (i + 64u < C && r1 < k) emit(r1, e1, mx);
+            }
+        }
     } else {
+    // the largest key, then ranks
+    {
+        uint32_t mx = 0;
+        for (uint32_t i = tid; i < C; i += kBlock) mx = max(mx, list[i].x);
+        atomicMax(&sm.maxkey, mx);
+        lds_sync();
+    }
+    const uint32_t mx = sm.maxkey;
     uint32_t G = 1u;
     while (G < 8u && C * G * 2u <= (uint32_t)kBlock) G <<= 1;
     for (uint32_t base = 0; base < C * G; base += kBlock) {
@@ -1469,9 +1577,10 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             r += r1;
         }
         for (uint32_t o = 1u; o < G; o <<= 1) r += __shfl_xor(r, (int)o, 64);
-        if (i < C && part == 0u && r < k) emit(r, e);
+        if (i < C && part == 0u && r < k) emit(r, e, mx);
     }
     }
+    PHASE_MARK(14);
     const uint32_t n_out = C < k ? C : k;
     lds_sync();
     PHASE_MARK(8);
