@@ -593,6 +593,13 @@ __device__ __forceinline__ RowIo load_row_io(const StepArgs &a, uint32_t row) {
 // Writes the output record, optional survivors / probabilities, the stream
 // control tick and the output ring. Runs on NT threads; wave 0 does the
 // sequential running sums.
+// A candidate (order key, token id) as one unsigned 64-bit value, key in the
+// high word and the complemented id in the low word: a larger value is a
+// better entry (larger key, then smaller id), and 0 ranks below every
+// candidate (candidate keys are nonzero).
+__device__ __forceinline__ uint64_t cand_pack(uint32_t key, uint32_t id) { return ((uint64_t)key << 32) | (uint64_t)(~id); }
+__device__ __forceinline__ uint2 cand_entry(uint64_t p) { return make_uint2((uint32_t)(p >> 32), ~(uint32_t)p); }
+
 // Running sums of one wave's lane values in sequential order: lane l gets
 // (((c + w_0) + w_1) + ... + w_l), rounded after every add exactly as a
 // sequential loop rounds. Each step adds a lane's own value to the sum of its
@@ -880,11 +887,11 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     uint32_t *s_hash = s_dyn;                                      // [hash_slots], a multiple of 64
     vec_t *s_svec = (vec_t *)(s_hash + a.hash_slots);              // [kStageCap]
     uint32_t *s_sslot = (uint32_t *)(s_svec + kStageCap);          // [kStageCap]
-    uint2 *s_cand = (uint2 *)(s_sslot + kStageCap);                // [kStreamCandCap], later finish scratch
-    uint2 *s_sorted = s_cand + kStreamCandCap;                     // [kcap]
+    uint64_t *s_cand = (uint64_t *)(s_sslot + kStageCap);          // [kStreamCandCap] packed, later finish scratch
+    uint2 *s_sorted = (uint2 *)(s_cand + kStreamCandCap);          // [kcap]
     uint32_t *s_pen = (uint32_t *)(s_sorted + a.kcap);             // [bitmap_words] when PEN != 0
     uint32_t *s_allow = s_pen + (PEN != 0 ? a.bitmap_words : 0u);  // [bitmap_words] with a mask
-    uint2 *s_big = s_cand;
+    uint2 *s_big = (uint2 *)s_cand;
 
     const uint32_t tid = threadIdx.x;
     const uint32_t logical = xcd_remap(blockIdx.x, gridDim.x);
@@ -978,7 +985,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         for (uint32_t i = tid; i < bm_n; i += kBlock) s_pen[i] = 0u;  // (bm_n need not be a multiple of 4)
     }
     // the candidate list reads as zero past its end (the rank sort's padding)
-    if (tid < kRankPad) s_cand[tid] = make_uint2(0u, 0u);
+    if (tid < kRankPad) s_cand[tid] = 0u;
     if (tid == 0) {
         sm.flag[1] = 0u;  // candidates
         sm.flag[2] = 0u;  // staged lane-vectors
@@ -1246,7 +1253,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     // the history state
     auto push = [&](uint32_t key, uint32_t id) __attribute__((always_inline)) {
         const uint32_t pos = atomicAdd(&sm.flag[1], 1u);
-        if (pos < kStreamCandCap) s_cand[pos] = make_uint2(key, id);
+        if (pos < kStreamCandCap) s_cand[pos] = cand_pack(key, id);
     };
     auto count_of = [&](uint32_t id) __attribute__((always_inline)) -> uint32_t {
         return history ? 1u + hash_lookup(s_hash, a.log2_slots, id) : 1u;
@@ -1279,33 +1286,38 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             const uint32_t key = elem_key(tail_bits, tail_id);
             if (key >= thr && key != 0u) push(key, tail_id);
         }
-        // One staged lane-vector per lane, spread over the waves (vector i
-        // to wave i % 8). A raw key below thr cannot qualify (the configured
-        // value of a token in the vector passes never exceeds its raw value),
-        // so only raw keys >= thr are examined further. Masked tokens of
-        // greedy rows count as -inf, which only a threshold at or below -inf
-        // admits: then every element is examined. The EPV ids of a
-        // lane-vector share one word of each bitmap; penalised ones (rare)
-        // take the table lookup. Appends are counted per wave: one LDS atomic
-        // per wave and round.
+        // Staged lane-vectors are spread over the waves (vector i to wave
+        // i % 8), kLPV lanes per vector, kEPL elements per lane. A raw key
+        // below thr cannot qualify (the configured value of a token in the
+        // vector passes never exceeds its raw value), so only raw keys >= thr
+        // are examined further. Masked tokens of greedy rows count as -inf,
+        // which only a threshold at or below -inf admits: then every element
+        // is examined. The ids of a lane-vector share one word of each
+        // bitmap; penalised ones (rare) take the table lookup. Appends are
+        // counted per wave: one LDS atomic per wave and round.
+        constexpr uint32_t kLPV = EPV >= 4 ? 4u : 1u, kEPL = (uint32_t)EPV / kLPV;
+        static_assert(kEPL <= 2u, "at most two elements per lane");
+        constexpr uint32_t kElemMask = (1u << kEPL) - 1u;
         const uint32_t thr_raw = thr > kNegInfKey ? thr : 0u;  // the raw-key prefilter
-        constexpr uint32_t kElemMask = (1u << EPV) - 1u;
-        for (uint32_t base = 0; base < nstaged; base += kBlock) {
-            const uint32_t i = base + lane * (uint32_t)kWaves + wave;
+        const uint32_t sub = lane % kLPV;
+        for (uint32_t base = 0; base < nstaged; base += (uint32_t)kBlock / kLPV) {
+            const uint32_t i = base + (lane / kLPV) * (uint32_t)kWaves + wave;
             const bool valid = i < nstaged;
             const uint32_t ic = valid ? i : 0u;
-            const vec_t v = s_svec[ic];
-            const uint32_t id0 = s_sslot[ic] * EPV;
+            const uint32_t e0 = sub * kEPL;  // first element of this lane
+            uint32_t bits[kEPL];
+            static_for<0, (int)kEPL>([&](auto E) __attribute__((always_inline)) { bits[E] = VT::staged_bits(s_svec, ic, e0 + (uint32_t)E); });
+            const uint32_t id0 = s_sslot[ic] * EPV + e0;
             const uint32_t off = id0 - bm_base;
             const uint32_t allow_bits = mask ? (s_allow[off >> 5] >> (off & 31u)) & kElemMask : kElemMask;
             uint32_t pen_bits = 0u;
             if constexpr (PEN != 0) pen_bits = (s_pen[off >> 5] >> (off & 31u)) & kElemMask;
             // branch-free: the key of every element, zero where it cannot qualify
-            uint32_t keys[EPV];
+            uint32_t keys[kEPL];
             uint32_t cand = 0u;
-            static_for<0, EPV>([&](auto E) __attribute__((always_inline)) {
+            static_for<0, (int)kEPL>([&](auto E) __attribute__((always_inline)) {
                 constexpr uint32_t bit = 1u << (int)E;
-                const uint32_t raw = raw_order_key(VT::bits(v, E));
+                const uint32_t raw = raw_order_key(bits[E]);
                 const bool c = valid && raw >= thr_raw;
                 cand |= c ? bit : 0u;
                 uint32_t key = (allow_bits & bit) ? raw : masked_key;
@@ -1319,16 +1331,17 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
                 pb &= pb - 1u;
                 uint32_t key = 0u;
                 if (lowering) {
-                    key = pen_key(VT::bits_dyn(v, e), ((allow_bits >> e) & 1u) != 0u, count_of(id0 + e));
+                    const uint32_t be = e == 0u ? bits[0] : bits[kEPL - 1u];  // kEPL <= 2
+                    key = pen_key(be, ((allow_bits >> e) & 1u) != 0u, count_of(id0 + e));
                     if (key < valid_min || key < thr) key = 0u;
                 }
-                static_for<0, EPV>([&](auto E) __attribute__((always_inline)) { keys[E] = e == (uint32_t)E ? key : keys[E]; });
+                static_for<0, (int)kEPL>([&](auto E) __attribute__((always_inline)) { keys[E] = e == (uint32_t)E ? key : keys[E]; });
             }
             uint32_t nq = 0u;
-            static_for<0, EPV>([&](auto E) __attribute__((always_inline)) { nq += keys[E] != 0u ? 1u : 0u; });
+            static_for<0, (int)kEPL>([&](auto E) __attribute__((always_inline)) { nq += keys[E] != 0u ? 1u : 0u; });
             // exclusive prefix and total of nq over the wave, bit by bit
             uint32_t excl = 0u, tot = 0u;
-            static_for<0, (EPV > 1 ? 4 : 1)>([&](auto B) __attribute__((always_inline)) {
+            static_for<0, (kEPL > 1u ? 2 : 1)>([&](auto B) __attribute__((always_inline)) {
                 const uint64_t m = __ballot((nq >> (int)B) & 1u);
                 excl += __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u)) << (int)B;
                 tot += (uint32_t)__builtin_popcountll(m) << (int)B;
@@ -1337,9 +1350,9 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
                 uint32_t pos0 = 0u;
                 if (lane == 0u) pos0 = atomicAdd(&sm.flag[1], tot);
                 uint32_t pos = (uint32_t)__builtin_amdgcn_readlane((int)pos0, 0) + excl;
-                static_for<0, EPV>([&](auto E) __attribute__((always_inline)) {
+                static_for<0, (int)kEPL>([&](auto E) __attribute__((always_inline)) {
                     if (keys[E] != 0u) {
-                        if (pos < kStreamCandCap) s_cand[pos] = make_uint2(keys[E], id0 + (uint32_t)E);
+                        if (pos < kStreamCandCap) s_cand[pos] = cand_pack(keys[E], id0 + (uint32_t)E);
                         ++pos;
                     }
                 });
@@ -1445,7 +1458,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             const uint32_t key = key_at(tt);
             if (key != 0u && (key > kv || (key == kv && need && tt <= id_cut))) {
                 const uint32_t q = atomicAdd(&sm.flag[1], 1u);
-                if (q < kStreamCandCap) s_cand[q] = make_uint2(key, tt);
+                if (q < kStreamCandCap) s_cand[q] = cand_pack(key, tt);
             }
         }
         lds_sync();
@@ -1454,18 +1467,18 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     // Many candidates (a weak threshold): keep the entries at or above the
     // k-th largest key (LDS radix select) in the staging area, which is free
     // by now, so the rank sort below stays small.
-    uint2 *list = s_cand;
+    uint64_t *list = s_cand;
     constexpr uint32_t kTrimCap = kStageCap * (uint32_t)sizeof(vec_t) / 8u;
     if (C > 256u && C > 4u * k) {
-        auto cand_key = [&](uint32_t i) __attribute__((always_inline)) -> uint32_t { return s_cand[i].x; };
+        auto cand_key = [&](uint32_t i) __attribute__((always_inline)) -> uint32_t { return (uint32_t)(s_cand[i] >> 32); };
         uint32_t unused_count;
         const uint32_t kth = radix_threshold_fn(0u, C, k, sm.hist, sm.sel, unused_count, cand_key);
-        uint2 *s_trim = (uint2 *)s_svec;
+        uint64_t *s_trim = (uint64_t *)s_svec;
         if (tid == 0) sm.flag[0] = 0u;
         lds_sync();
         for (uint32_t i = tid; i < C; i += kBlock) {
-            const uint2 e = s_cand[i];
-            if (e.x >= kth) {
+            const uint64_t e = s_cand[i];
+            if ((uint32_t)(e >> 32) >= kth) {
                 const uint32_t q = atomicAdd(&sm.flag[0], 1u);
                 if (q < kTrimCap) s_trim[q] = e;
             }
@@ -1499,22 +1512,18 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         // entry_better; the list reads as (0, 0) past C, which ranks below
         // every candidate (keys are nonzero).
         if (repad) {
-            for (uint32_t i = C + tid; i < kRankPad; i += kBlock) list[i] = make_uint2(0u, 0u);
+            for (uint32_t i = C + tid; i < kRankPad; i += kBlock) list[i] = 0u;
             lds_sync();
         }
-        auto packed = [](uint2 e) __attribute__((always_inline)) -> uint64_t {
-            return ((uint64_t)e.x << 32) | (uint64_t)(~e.y);
-        };
         const uint32_t i = tid >> 3, part = tid & 7u;
-        const uint2 e0 = list[i];
-        const uint64_t p0 = packed(e0);
+        const uint64_t p0 = list[i];
         if (C <= 64u) {
-            uint2 o[8];
+            uint64_t o[8];
             static_for<0, 8>([&](auto J) __attribute__((always_inline)) { o[J] = list[part + 8u * (uint32_t)J]; });
             uint32_t r = 0, mx = 0;
             static_for<0, 8>([&](auto J) __attribute__((always_inline)) {
-                r += packed(o[J]) > p0 ? 1u : 0u;
-                mx = max(mx, o[J].x);
+                r += o[J] > p0 ? 1u : 0u;
+                mx = max(mx, (uint32_t)(o[J] >> 32));
             });
             // the 8 lanes of a group read the whole list: mx becomes its largest key
             r += __shfl_xor(r, 1, 64);
@@ -1523,18 +1532,16 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             mx = max(mx, (uint32_t)__shfl_xor((int)mx, 2, 64));
             r += __shfl_xor(r, 4, 64);
             mx = max(mx, (uint32_t)__shfl_xor((int)mx, 4, 64));
-            if (i < C && part == 0u && r < k) emit(r, e0, mx);
+            if (i < C && part == 0u && r < k) emit(r, cand_entry(p0), mx);
         } else {
-            const uint2 e1 = list[i + 64u];
-            const uint64_t p1 = packed(e1);
-            uint2 o[16];
+            const uint64_t p1 = list[i + 64u];
+            uint64_t o[16];
             static_for<0, 16>([&](auto J) __attribute__((always_inline)) { o[J] = list[part + 8u * (uint32_t)J]; });
             uint32_t r0 = 0, r1 = 0, mx = 0;
             static_for<0, 16>([&](auto J) __attribute__((always_inline)) {
-                const uint64_t po = packed(o[J]);
-                r0 += po > p0 ? 1u : 0u;
-                r1 += po > p1 ? 1u : 0u;
-                mx = max(mx, o[J].x);
+                r0 += o[J] > p0 ? 1u : 0u;
+                r1 += o[J] > p1 ? 1u : 0u;
+                mx = max(mx, (uint32_t)(o[J] >> 32));
             });
             r0 += __shfl_xor(r0, 1, 64);
             r1 += __shfl_xor(r1, 1, 64);
@@ -1546,15 +1553,15 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             r1 += __shfl_xor(r1, 4, 64);
             mx = max(mx, (uint32_t)__shfl_xor((int)mx, 4, 64));
             if (part == 0u) {
-                if (i < C && r0 < k) emit(r0, e0, mx);
-                if (i + 64u < C && r1 < k) emit(r1, e1, mx);
+                if (i < C && r0 < k) emit(r0, cand_entry(p0), mx);
+                if (i + 64u < C && r1 < k) emit(r1, cand_entry(p1), mx);
             }
         }
     } else {
     // the largest key, then ranks
     {
         uint32_t mx = 0;
-        for (uint32_t i = tid; i < C; i += kBlock) mx = max(mx, list[i].x);
+        for (uint32_t i = tid; i < C; i += kBlock) mx = max(mx, (uint32_t)(list[i] >> 32));
         atomicMax(&sm.maxkey, mx);
         lds_sync();
     }
@@ -1564,20 +1571,20 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     for (uint32_t base = 0; base < C * G; base += kBlock) {
         const uint32_t q = base + tid, i = q / G, part = q % G;
         uint32_t r = 0;
-        uint2 e = make_uint2(0u, 0u);
+        uint64_t e = 0u;
         if (i < C) {
             e = list[i];
             uint32_t r1 = 0;
             uint32_t j = part;
             for (; j + G < C; j += 2u * G) {
-                r += entry_better(list[j], e) ? 1u : 0u;
-                r1 += entry_better(list[j + G], e) ? 1u : 0u;
+                r += list[j] > e ? 1u : 0u;
+                r1 += list[j + G] > e ? 1u : 0u;
             }
-            if (j < C) r += entry_better(list[j], e) ? 1u : 0u;
+            if (j < C) r += list[j] > e ? 1u : 0u;
             r += r1;
         }
         for (uint32_t o = 1u; o < G; o <<= 1) r += __shfl_xor(r, (int)o, 64);
-        if (i < C && part == 0u && r < k) emit(r, e, mx);
+        if (i < C && part == 0u && r < k) emit(r, cand_entry(e), mx);
     }
     }
     PHASE_MARK(14);
