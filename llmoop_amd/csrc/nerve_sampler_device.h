@@ -550,7 +550,6 @@ struct SharedSmall {
     uint32_t ukeys[2][kWaves * 64];  // report unions of the two threshold passes
     uint32_t ucount[2][kWaves];
     uint32_t uthr[2];
-    uint32_t maxkey;
     float u;  // the row's uniform draw
 };
 
@@ -600,6 +599,16 @@ __device__ __forceinline__ RowIo load_row_io(const StepArgs &a, uint32_t row) {
 __device__ __forceinline__ uint64_t cand_pack(uint32_t key, uint32_t id) { return ((uint64_t)key << 32) | (uint64_t)(~id); }
 __device__ __forceinline__ uint2 cand_entry(uint64_t p) { return make_uint2((uint32_t)(p >> 32), ~(uint32_t)p); }
 
+// Sum of r over each aligned group of 8 lanes, valid in the group's first
+// lane (row shifts toward lower lanes: dpp_ctrl 0x101/0x102/0x104 are
+// row_shl:1/2/4; lanes past a row's end read 0).
+__device__ __forceinline__ uint32_t group8_sum(uint32_t r) {
+    r += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)r, 0x101, 0xf, 0xf, true);
+    r += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)r, 0x102, 0xf, 0xf, true);
+    r += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)r, 0x104, 0xf, 0xf, true);
+    return r;
+}
+
 // Running sums of one wave's lane values in sequential order: lane l gets
 // (((c + w_0) + w_1) + ... + w_l), rounded after every add exactly as a
 // sequential loop rounds. Each step adds a lane's own value to the sum of its
@@ -623,8 +632,7 @@ template <typename Elem, int PEN, int NT>
 __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, const RowIo &io, const nerve_sampler_row_params &P, uint32_t k,
                            bool sampled, uint32_t n, uint32_t row_flags, uint2 *s_sorted, uint2 *s_big,
                            float *s_w, float *s_p, uint32_t *s_hash, const RowCtx &ctx, float u) {
-    // s_w [kcap + 64]: the weights of s_sorted[0 .. n), written by the caller
-    // (the rest are computed here), then zero past the min-p cut.
+    // s_w [kcap]: weights, zero past the min-p cut (more than 64 survivors)
     // s_p [kcap]: running sums, then probabilities.
     const uint32_t tid = threadIdx.x;
     uint32_t token = 0, sel_bits = 0, out_flags = 0, kout = 1;
@@ -715,7 +723,7 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
             const uint64_t below = __ballot(live && v < minimum);
             if (below) n_valid = (uint32_t)__builtin_ctzll(below);
             float w = 0.0f;
-            if (lane < n_valid) w = lane < n ? s_w[lane] : nerve_expf(v / T - m);  // padding entries computed here
+            if (lane < n_valid) w = nerve_expf(v / T - m);
             const float acc = sequential_prefix(w, 0.0f, n_valid);
             PHASE_MARK(10);
             const float total = n_valid ? u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(n_valid - 1u))) : 0.0f;
@@ -746,7 +754,7 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
                 if (c0 >= n_valid) break;
                 const bool in = i < n_valid;
                 float w = 0.0f;
-                if (in) w = i < n ? s_w[i] : nerve_expf(v / T - m);
+                if (in) w = nerve_expf(v / T - m);
                 if (i < k) s_w[i] = w;
                 const uint32_t len = min(64u, n_valid - c0);
                 const float acc = sequential_prefix(w, carry, len);
@@ -990,7 +998,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         sm.flag[1] = 0u;  // candidates
         sm.flag[2] = 0u;  // staged lane-vectors
         sm.flag[3] = 0u;  // slice flags
-        sm.maxkey = 0u;   // largest candidate key
         sm.ones[0] = 0xffffffffu;
         sm.io[0] = io.seed;
         sm.io[1] = io.tick_lo;
@@ -1491,15 +1498,10 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         }
     }
     // The writer of rank r also settles the sign of a zero survivor (from its
-    // own configured value) and, for sampled rows, computes its weight
-    // exp(l / T - m) with m = l0 / T from the largest candidate key (the sign
-    // of a zero l cannot change a weight).
-    float *s_wt = (float *)s_sslot;  // [kcap + 64], the staging slots are free by now
-    const float T = P.temperature;
-    auto emit = [&](uint32_t r, uint2 e, uint32_t maxkey) __attribute__((always_inline)) {
+    // own configured value).
+    auto emit = [&](uint32_t r, uint2 e) __attribute__((always_inline)) {
         if (e.x == kZeroKey && f2u(configured_at<Elem>(ctx, e.y)) == 0x80000000u) e.y |= kNegZeroFlag;
         s_sorted[r] = e;
-        if (sampled && a.slices == 1u) s_wt[r] = nerve_expf(entry_value(e) / T - key_to_float(maxkey) / T);
     };
     // rank sort (ids are distinct, so ranks are a permutation): G adjacent
     // lanes share a candidate, each counting the better entries in every G-th
@@ -1508,7 +1510,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     if (C <= kRankPad) {
         // The common case, unrolled: 8 adjacent lanes share a candidate (two,
         // i and i + 64, past 64 candidates), each comparing it with every 8th
-        // list entry. (key, ~id) as one unsigned 64-bit value orders like
+        // list entry, and the group's first lane sums the counts. (key, ~id) as one unsigned 64-bit value orders like
         // entry_better; the list reads as (0, 0) past C, which ranks below
         // every candidate (keys are nonzero).
         if (repad) {
@@ -1520,52 +1522,27 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         if (C <= 64u) {
             uint64_t o[8];
             static_for<0, 8>([&](auto J) __attribute__((always_inline)) { o[J] = list[part + 8u * (uint32_t)J]; });
-            uint32_t r = 0, mx = 0;
-            static_for<0, 8>([&](auto J) __attribute__((always_inline)) {
-                r += o[J] > p0 ? 1u : 0u;
-                mx = max(mx, (uint32_t)(o[J] >> 32));
-            });
-            // the 8 lanes of a group read the whole list: mx becomes its largest key
-            r += __shfl_xor(r, 1, 64);
-            mx = max(mx, (uint32_t)__shfl_xor((int)mx, 1, 64));
-            r += __shfl_xor(r, 2, 64);
-            mx = max(mx, (uint32_t)__shfl_xor((int)mx, 2, 64));
-            r += __shfl_xor(r, 4, 64);
-            mx = max(mx, (uint32_t)__shfl_xor((int)mx, 4, 64));
-            if (i < C && part == 0u && r < k) emit(r, cand_entry(p0), mx);
+            uint32_t r = 0;
+            static_for<0, 8>([&](auto J) __attribute__((always_inline)) { r += o[J] > p0 ? 1u : 0u; });
+            r = group8_sum(r);
+            if (i < C && part == 0u && r < k) emit(r, cand_entry(p0));
         } else {
             const uint64_t p1 = list[i + 64u];
             uint64_t o[16];
             static_for<0, 16>([&](auto J) __attribute__((always_inline)) { o[J] = list[part + 8u * (uint32_t)J]; });
-            uint32_t r0 = 0, r1 = 0, mx = 0;
+            uint32_t r0 = 0, r1 = 0;
             static_for<0, 16>([&](auto J) __attribute__((always_inline)) {
                 r0 += o[J] > p0 ? 1u : 0u;
                 r1 += o[J] > p1 ? 1u : 0u;
-                mx = max(mx, (uint32_t)(o[J] >> 32));
             });
-            r0 += __shfl_xor(r0, 1, 64);
-            r1 += __shfl_xor(r1, 1, 64);
-            mx = max(mx, (uint32_t)__shfl_xor((int)mx, 1, 64));
-            r0 += __shfl_xor(r0, 2, 64);
-            r1 += __shfl_xor(r1, 2, 64);
-            mx = max(mx, (uint32_t)__shfl_xor((int)mx, 2, 64));
-            r0 += __shfl_xor(r0, 4, 64);
-            r1 += __shfl_xor(r1, 4, 64);
-            mx = max(mx, (uint32_t)__shfl_xor((int)mx, 4, 64));
+            r0 = group8_sum(r0);
+            r1 = group8_sum(r1);
             if (part == 0u) {
-                if (i < C && r0 < k) emit(r0, cand_entry(p0), mx);
-                if (i + 64u < C && r1 < k) emit(r1, cand_entry(p1), mx);
+                if (i < C && r0 < k) emit(r0, cand_entry(p0));
+                if (i + 64u < C && r1 < k) emit(r1, cand_entry(p1));
             }
         }
     } else {
-    // the largest key, then ranks
-    {
-        uint32_t mx = 0;
-        for (uint32_t i = tid; i < C; i += kBlock) mx = max(mx, (uint32_t)(list[i] >> 32));
-        atomicMax(&sm.maxkey, mx);
-        lds_sync();
-    }
-    const uint32_t mx = sm.maxkey;
     uint32_t G = 1u;
     while (G < 8u && C * G * 2u <= (uint32_t)kBlock) G <<= 1;
     for (uint32_t base = 0; base < C * G; base += kBlock) {
@@ -1584,7 +1561,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             r += r1;
         }
         for (uint32_t o = 1u; o < G; o <<= 1) r += __shfl_xor(r, (int)o, 64);
-        if (i < C && part == 0u && r < k) emit(r, cand_entry(e), mx);
+        if (i < C && part == 0u && r < k) emit(r, cand_entry(e));
     }
     }
     PHASE_MARK(14);
@@ -1603,7 +1580,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         return;
     }
     const RowIo io_l = {sm.io[0], sm.io[1], sm.io[2], sm.io[3]};
-    finish_row<Elem, PEN, kBlock>(a, row, io_l, P, k, sampled, n_out, flags_slice, s_sorted, s_big, s_wt,
+    finish_row<Elem, PEN, kBlock>(a, row, io_l, P, k, sampled, n_out, flags_slice, s_sorted, s_big, (float *)s_sslot,
                                   (float *)s_big + 64, s_hash, ctx, sm.u);
     PHASE_MARK(12);
 }
@@ -1617,7 +1594,7 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
     uint32_t *s_hash = s_dyn;
     uint2 *s_big = (uint2 *)(s_dyn + a.hash_slots);
     uint2 *s_sorted = s_big + a.big_entries;
-    float *s_wt = (float *)(s_sorted + a.kcap);  // [kcap + 64] weights of the merged list
+    float *s_wt = (float *)(s_sorted + a.kcap);  // [kcap] weights
     const uint32_t tid = threadIdx.x;
     const uint32_t row = blockIdx.x;
     const nerve_sampler_row_params P = a.params[row];
@@ -1629,15 +1606,12 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
 
     const uint2 *all = a.scratch_lists + (uint64_t)row * a.slices * a.kcap;
     const uint32_t *meta = a.scratch_meta + row * a.slices;
-    uint32_t total = 0, row_flags = 0, maxkey = 0;
+    uint32_t total = 0, row_flags = 0;
     for (uint32_t s = 0; s < a.slices; ++s) {
         const uint32_t m = meta[s];
         total += m & 0xffffu;
         row_flags |= m >> 16;
-        if (m & 0xffffu) maxkey = max(maxkey, all[(uint64_t)s * a.kcap].x);  // the head of a sorted list
     }
-    const float T = P.temperature;
-    const float m_w = sampled ? key_to_float(maxkey) / T : 0.0f;
     const uint32_t ne = a.slices * a.kcap;
     for (uint32_t i = tid; i < ne; i += kFinishBlock) {
         const uint32_t s = i / a.kcap, pos = i % a.kcap;
@@ -1661,10 +1635,7 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
             }
             r += lo_i;
         }
-        if (r < k) {
-            s_sorted[r] = e;
-            if (sampled) s_wt[r] = nerve_expf(entry_value(e) / T - m_w);
-        }
+        if (r < k) s_sorted[r] = e;
     }
     const uint32_t n = total < k ? total : k;
     __syncthreads();
