@@ -990,7 +990,9 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     if constexpr (history) {
         const uint4 empty4 = make_uint4(kHashEmpty, kHashEmpty, kHashEmpty, kHashEmpty);
         for (uint32_t i = tid; i < a.hash_slots / 4u; i += kBlock) ((uint4 *)s_hash)[i] = empty4;
-        for (uint32_t i = tid; i < bm_n; i += kBlock) s_pen[i] = 0u;  // (bm_n need not be a multiple of 4)
+        // the bitmap is 8-byte aligned: zero it in pairs of words
+        for (uint32_t i = tid; i < bm_n / 2u; i += kBlock) ((uint2 *)s_pen)[i] = make_uint2(0u, 0u);
+        if ((bm_n & 1u) && tid == 0) s_pen[bm_n - 1u] = 0u;
     }
     // the candidate list reads as zero past its end (the rank sort's padding)
     if (tid < kRankPad) s_cand[tid] = 0u;

@@ -205,3 +205,36 @@ def test_penalised_top_tokens_take_the_exact_path(oracle, dtype):
     # no survivor is one of the penalised top tokens
     for r in range(B):
         assert not set(gpu["topk_ids"][r][:50]) & set(hist[r, :150].tolist())
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_many_repeated_history_ids(oracle, dtype):
+    """Each row's history repeats its top raw tokens many times (hundreds of
+    occurrences beyond the first), so the repeat counts go through the table
+    rather than the short scan, and the frequency penalty separates tokens by
+    their counts."""
+    from llmoop_amd.workloads import to_bf16_bits
+
+    rng = np.random.default_rng(57)
+    B, V, H = 6, 30000, 512
+    x = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
+    hist = np.zeros((B, H), np.uint32)
+    for r in range(B):
+        top = np.argsort(-x[r])[:40]
+        reps = np.repeat(top, rng.integers(1, 12, top.size))[:H]
+        hist[r, :reps.size] = reps
+        hist[r, reps.size:] = rng.integers(0, V, H - reps.size)
+        rng.shuffle(hist[r])
+    logits = to_bf16_bits(x) if dtype == "bf16" else x
+    params = _random_params(rng, B, 64, method=1)
+    params["top_k"] = 40
+    params["repetition_penalty"] = 1.05
+    params["frequency_penalty"] = 0.15
+    params["presence_penalty"] = 0.1
+    kw = dict(history=hist, history_len=np.full(B, H, np.uint32),
+              seeds=rng.integers(0, 2**32, B, dtype=np.uint64).astype(np.uint32),
+              steps=rng.integers(0, 2**40, B, dtype=np.uint64))
+    _say(f"many repeated history ids {dtype}")
+    ref = oracle.sample(logits, params, top_k_capacity=64, **kw)
+    gpu = run_gpu(logits, params, top_k_capacity=64, **kw)
+    assert_parity(gpu, ref, params, label="many-repeats", prob_rtol=1e-5 if dtype == "f32" else 2e-3)
