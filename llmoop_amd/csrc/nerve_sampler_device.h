@@ -1197,6 +1197,10 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         if constexpr (j + D < NV) load(j + D);
         if constexpr ((j & 7) == 0) flags_at(std::integral_constant<int, j>{});
         pass1(j);
+        // without a mask, keep each load in its step: hoisting the first
+        // half's loads (the compiler's choice) puts too many in flight and
+        // slows the stream (measured; with a mask the hoisting pays)
+        if constexpr (!MASK) __builtin_amdgcn_sched_barrier(0);
     };
     static_for<0, NA>(step_in);
     set_thr(report_threshold(0));
