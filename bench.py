@@ -58,6 +58,7 @@ def parse():
     ap.add_argument("--buffers", type=int, default=4, help="logits copies the steps rotate over")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="host threads of the CPU baseline (0: up to 16)")
     ap.add_argument("--slices", type=int, default=0, help="workgroups per row (0 = automatic)")
     ap.add_argument("--variant", default="", help="diagnostics: no-history | greedy | no-penalty")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
@@ -66,12 +67,12 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(w, budget_s: float) -> dict:
+def cpu_baseline(w, budget_s: float, threads: int = 0) -> dict:
     """The oracle (a C restatement of the reference semantics, -O3, OpenMP
     over rows) on the host cores: as many full-batch steps as fit the budget."""
     from oracle import oracle
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = threads or min(os.cpu_count() or 1, 16)
     kw = dict(history=w.history, history_len=w.history_len, allowed=w.allowed, seeds=w.seeds)
     done_rows = 0
     t0 = time.perf_counter()
@@ -268,7 +269,7 @@ def main():
         },
     }
     if not args.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
+        res["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds, args.cpu_threads)
     print(json.dumps(res), flush=True)
 
 
