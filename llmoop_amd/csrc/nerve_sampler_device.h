@@ -1610,18 +1610,17 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
     k = k < 1u ? 1u : (k > a.kcap ? a.kcap : k);
     const float u = sampled ? random_unit(a.rng, io.seed, (uint64_t)io.tick_lo | ((uint64_t)io.tick_hi << 32), row) : 0.0f;
 
+    // every list entry is copied, whatever the counts (entries past a count
+    // are ignored below), so the list loads do not wait for the counts
     const uint2 *all = a.scratch_lists + (uint64_t)row * a.slices * a.kcap;
     const uint32_t *meta = a.scratch_meta + row * a.slices;
+    const uint32_t ne = a.slices * a.kcap;
+    for (uint32_t i = tid; i < ne; i += kFinishBlock) s_big[i] = all[i];
     uint32_t total = 0, row_flags = 0;
     for (uint32_t s = 0; s < a.slices; ++s) {
         const uint32_t m = meta[s];
         total += m & 0xffffu;
         row_flags |= m >> 16;
-    }
-    const uint32_t ne = a.slices * a.kcap;
-    for (uint32_t i = tid; i < ne; i += kFinishBlock) {
-        const uint32_t s = i / a.kcap, pos = i % a.kcap;
-        if (pos < (meta[s] & 0xffffu)) s_big[i] = all[i];
     }
     __syncthreads();
     // rank of an entry = its position in its own sorted list plus the number
