@@ -194,18 +194,14 @@ int nerve_sampler_create(const nerve_sampler_desc *desc, nerve_sampler **out) {
         return fail(NERVE_ERR_HIP, std::string("the sampler kernels are built for gfx950 only, device is ") + prop.gcnArchName);
 
     // Workgroups per row: a workgroup holds its slice of the row in VGPRs, so
-    // a slice is at most block_threads() * max_vectors_per_lane() lane-vectors;
-    // small batches split rows further so the launch still covers the CUs.
+    // a slice is at most block_threads() * max_vectors_per_lane() lane-vectors
+    // (raised per step to what the row needs). Automatic: one slice where the
+    // row fits, since a second slice costs the merge launch, which measured
+    // more than the bandwidth it adds at small batches (C1 8.6 vs 10.5 µs, C2
+    // 11.0 vs 14.1 µs on MI355X).
     const uint32_t threads = nerve::block_threads();
     uint32_t want = d.slices_per_row;
-    if (want == 0u) {
-        const uint32_t cus = (uint32_t)prop.multiProcessorCount;
-        want = cus / d.max_batch;
-        const uint32_t by_size = d.vocab_size / (threads * 16u);  // keep >= 16 elements per lane
-        if (want > by_size) want = by_size;
-        if (want > 64u) want = 64u;
-        if (want == 0u) want = 1u;
-    }
+    if (want == 0u) want = 1u;
     // The one-element-per-load kernels hold the fewest tokens per slice.
     const uint32_t scalar_tokens = threads * nerve::max_vectors_per_lane(nerve::kVariantF32Scalar);
     const uint32_t need = (d.vocab_size + scalar_tokens - 1u) / scalar_tokens;
