@@ -871,8 +871,10 @@ __host__ __device__ constexpr uint32_t slice_bitmap_words(uint32_t tokens, uint3
 //   select  after the first half: every wave's top reports go to an LDS union
 //           and its k-th largest key becomes thr;
 //   pass 2  lane-vectors whose raw maximum reaches thr are staged in LDS;
-//   exact   one lane per staged element computes its configured key (mask,
-//           penalties) and appends keys >= thr to the candidate list.
+//   exact   four lanes per staged lane-vector compute the configured keys
+//           (mask, penalties) and append keys >= thr to the candidate list;
+//   rank    a rank sort of the candidates writes the top k in order;
+//   finish  wave 0: weights, sequential running sums, nucleus, draw, record.
 // The top k are all candidates exactly when at least k configured keys reach
 // thr; a slice where penalties pushed too many reported values below thr
 // takes the exact selection from memory instead. Penalties that never raise
