@@ -1088,8 +1088,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     const uint32_t wsh = tok_base & 31u;
     const uint32_t *allow_w = s_allow + (tok_base >> 5);
     constexpr uint32_t kWordsPerJ = 64u * EPV / 32u;
-    auto flags_group = [&](auto mask_tag, auto J0) __attribute__((always_inline)) {
-        constexpr bool M = decltype(mask_tag)::value;
+    auto flags_group = [&](auto J0) __attribute__((always_inline)) {
         constexpr int j0 = decltype(J0)::value;
         uint32_t aw[8];
 #pragma unroll
@@ -1106,7 +1105,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         live[j0 >> 5] &= ~(0xffu << sh) | (lvg << sh);
     };
     auto flags_at = [&](auto J0) __attribute__((always_inline)) {
-        if constexpr (MASK) flags_group(std::true_type{}, J0);
+        if constexpr (MASK) flags_group(J0);
     };
     uint32_t acc0 = VT::kAccInit, acc1 = VT::kAccInit;
     // vmx[j]: the raw signed-integer maximum of lane-vector j, computed once
