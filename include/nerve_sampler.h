@@ -123,7 +123,8 @@ typedef struct {
     uint32_t dtype;             /* NERVE_DTYPE_* of the logits */
     uint32_t top_k_capacity;    /* 1..NERVE_MAX_TOP_K_CAPACITY */
     uint32_t history_capacity;  /* max history ids per row, 0..NERVE_MAX_HISTORY_CAPACITY */
-    uint32_t slices_per_row;    /* 0 = automatic; workgroups cooperating on one row */
+    uint32_t slices_per_row;    /* workgroups cooperating on one row; 0 = automatic: one, or the
+                                   fewest whose registers hold the row (raised per step as needed) */
     uint32_t device;            /* HIP device ordinal */
     uint32_t reserved;
 } nerve_sampler_desc;
