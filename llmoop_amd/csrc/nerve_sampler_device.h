@@ -481,7 +481,7 @@ __device__ __forceinline__ uint32_t radix_threshold(const uint32_t (&v)[N], uint
 // exact path, which recomputes keys from memory instead of holding them.
 template <typename KeyFn>
 __device__ __forceinline__ uint32_t radix_threshold_fn(uint32_t t0, uint32_t t1, uint32_t k, uint32_t *s_hist, uint32_t *s_sel,
-                                       uint32_t &count_ge, KeyFn key_of) {
+                                       uint32_t &count_ge, KeyFn key_of, uint32_t *count_gt = nullptr) {
     const uint32_t tid = threadIdx.x;
     uint32_t prefix = 0, remaining = k, above_total = 0;
     count_ge = 0;
@@ -490,9 +490,18 @@ __device__ __forceinline__ uint32_t radix_threshold_fn(uint32_t t0, uint32_t t1,
         const uint32_t hmask = p == 0 ? 0u : (0xffffffffu << (shift + 8));
         for (uint32_t i = tid; i < 256u; i += kBlock) s_hist[i] = 0u;
         lds_sync();
-        for (uint32_t t = t0 + tid; t < t1; t += kBlock) {
-            const uint32_t x = key_of(t);
-            if (x != 0u && (x & hmask) == prefix) atomicAdd(&s_hist[(x >> shift) & 255u], 1u);
+        // 8 keys per lane and round, all computed before any count, so their
+        // memory reads overlap
+        for (uint32_t t = t0 + tid; t < t1; t += 8u * kBlock) {
+            uint32_t x[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t tt = t + (uint32_t)u * kBlock;
+                x[u] = tt < t1 ? key_of(tt) : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (x[u] != 0u && (x[u] & hmask) == prefix) atomicAdd(&s_hist[(x[u] >> shift) & 255u], 1u);
         }
         lds_sync();
         if (tid < 64) {
@@ -527,6 +536,7 @@ __device__ __forceinline__ uint32_t radix_threshold_fn(uint32_t t0, uint32_t t1,
         lds_sync();
         if (d == 0xffffffffu) {
             count_ge = above_total + above;
+            if (count_gt) *count_gt = count_ge;
             return 1u;
         }
         remaining -= above;
@@ -534,6 +544,7 @@ __device__ __forceinline__ uint32_t radix_threshold_fn(uint32_t t0, uint32_t t1,
         prefix |= d << shift;
         count_ge = above_total + in_bin;
     }
+    if (count_gt) *count_gt = above_total;
     return prefix;
 }
 
@@ -1462,22 +1473,31 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             return key < valid_min ? 0u : key;
         };
         repad = true;
-        uint32_t count_ge;
-        const uint32_t kv = radix_threshold_fn(tok0, tok1, k, sm.hist, sm.sel, count_ge, key_at);
-        uint32_t gt = 0;
-        for (uint32_t tt = tok0 + tid; tt < tok1; tt += kBlock) gt += key_at(tt) > kv ? 1u : 0u;
-        const uint32_t G = block_sum(gt, sm.scan);
+        uint32_t count_ge, G;
+        const uint32_t kv = radix_threshold_fn(tok0, tok1, k, sm.hist, sm.sel, count_ge, key_at, &G);
+        // G keys above kv; `need` of the count_ge - G ties at kv qualify: all
+        // of them when they fit, else the `need` smallest ids
         const uint32_t need = k > G ? k - G : 0u;
         auto tie_at = [&](uint32_t tt) __attribute__((always_inline)) -> uint32_t { return key_at(tt) == kv ? ~tt : 0u; };
         uint32_t ties_ge;
-        const uint32_t id_cut = need ? ~radix_threshold_fn(tok0, tok1, need, sm.hist, sm.sel, ties_ge, tie_at) : 0u;
+        uint32_t id_cut = 0xffffffffu;
+        if (need && count_ge - G > need) id_cut = ~radix_threshold_fn(tok0, tok1, need, sm.hist, sm.sel, ties_ge, tie_at);
         if (tid == 0) sm.flag[1] = 0u;
         lds_sync();
-        for (uint32_t tt = tok0 + tid; tt < tok1; tt += kBlock) {
-            const uint32_t key = key_at(tt);
-            if (key != 0u && (key > kv || (key == kv && need && tt <= id_cut))) {
-                const uint32_t q = atomicAdd(&sm.flag[1], 1u);
-                if (q < kStreamCandCap) s_cand[q] = cand_pack(key, tt);
+        for (uint32_t t0c = tok0 + tid; t0c < tok1; t0c += 8u * kBlock) {
+            uint32_t keys[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t tt = t0c + (uint32_t)u * kBlock;
+                keys[u] = tt < tok1 ? key_at(tt) : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t tt = t0c + (uint32_t)u * kBlock, key = keys[u];
+                if (key != 0u && (key > kv || (key == kv && need && tt <= id_cut))) {
+                    const uint32_t q = atomicAdd(&sm.flag[1], 1u);
+                    if (q < kStreamCandCap) s_cand[q] = cand_pack(key, tt);
+                }
             }
         }
         lds_sync();
