@@ -479,9 +479,10 @@ __device__ __forceinline__ uint32_t radix_threshold(const uint32_t (&v)[N], uint
 // Same contract as radix_threshold (all four bytes), over the tokens
 // [t0, t1) of a slice with keys produced by `key_of(t)`; used by the rare
 // exact path, which recomputes keys from memory instead of holding them.
-template <typename KeyFn>
-__device__ __forceinline__ uint32_t radix_threshold_fn(uint32_t t0, uint32_t t1, uint32_t k, uint32_t *s_hist, uint32_t *s_sel,
-                                       uint32_t &count_ge, KeyFn key_of, uint32_t *count_gt = nullptr) {
+// visit(fn) calls fn(key) for every key this thread holds (0: no key).
+template <typename VisitFn>
+__device__ __forceinline__ uint32_t radix_threshold_visit(uint32_t k, uint32_t *s_hist, uint32_t *s_sel, uint32_t &count_ge,
+                                                          VisitFn visit, uint32_t *count_gt = nullptr) {
     const uint32_t tid = threadIdx.x;
     uint32_t prefix = 0, remaining = k, above_total = 0;
     count_ge = 0;
@@ -490,19 +491,9 @@ __device__ __forceinline__ uint32_t radix_threshold_fn(uint32_t t0, uint32_t t1,
         const uint32_t hmask = p == 0 ? 0u : (0xffffffffu << (shift + 8));
         for (uint32_t i = tid; i < 256u; i += kBlock) s_hist[i] = 0u;
         lds_sync();
-        // 8 keys per lane and round, all computed before any count, so their
-        // memory reads overlap
-        for (uint32_t t = t0 + tid; t < t1; t += 8u * kBlock) {
-            uint32_t x[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const uint32_t tt = t + (uint32_t)u * kBlock;
-                x[u] = tt < t1 ? key_of(tt) : 0u;
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (x[u] != 0u && (x[u] & hmask) == prefix) atomicAdd(&s_hist[(x[u] >> shift) & 255u], 1u);
-        }
+        visit([&](uint32_t x) __attribute__((always_inline)) {
+            if (x != 0u && (x & hmask) == prefix) atomicAdd(&s_hist[(x >> shift) & 255u], 1u);
+        });
         lds_sync();
         if (tid < 64) {
             const uint32_t lane = tid;
@@ -546,6 +537,27 @@ __device__ __forceinline__ uint32_t radix_threshold_fn(uint32_t t0, uint32_t t1,
     }
     if (count_gt) *count_gt = above_total;
     return prefix;
+}
+
+// The same over the tokens [t0, t1) of a slice with keys key_of(t).
+template <typename KeyFn>
+__device__ __forceinline__ uint32_t radix_threshold_fn(uint32_t t0, uint32_t t1, uint32_t k, uint32_t *s_hist, uint32_t *s_sel,
+                                       uint32_t &count_ge, KeyFn key_of, uint32_t *count_gt = nullptr) {
+    const uint32_t tid = threadIdx.x;
+    auto visit = [&](auto &&fn) __attribute__((always_inline)) {
+        // 8 keys per lane and round, all computed before any count
+        for (uint32_t t = t0 + tid; t < t1; t += 8u * kBlock) {
+            uint32_t x[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t tt = t + (uint32_t)u * kBlock;
+                x[u] = tt < t1 ? key_of(tt) : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) fn(x[u]);
+        }
+    };
+    return radix_threshold_visit(k, s_hist, s_sel, count_ge, visit, count_gt);
 }
 
 // ---- the fused kernel -------------------------------------------------------
@@ -1468,38 +1480,80 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         // more than C - k of the reported values below thr: exact selection
         // recomputed from memory. The k-th largest key kv, then the `need`
         // smallest ids among keys == kv.
-        auto key_at = [&](uint32_t tt) __attribute__((always_inline)) -> uint32_t {
-            const uint32_t key = order_key(configured_at<Elem>(ctx, tt));
-            return key < valid_min ? 0u : key;
+        // Every (key, id) of the slice, read back like the stream: chunks of 8
+        // lane-vectors through the wave's buffer resource, one bitmap word per
+        // lane-vector, and the configured key of each element (penalised ones
+        // from their counts); then the V % EPV tail.
+        auto each_key = [&](auto &&fn) __attribute__((always_inline)) {
+            for (uint32_t j = 0; j < nval; j += 4u) {
+                vec_t v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t off = (lane + (j + (uint32_t)u) * 64u) * kVecBytes;
+                    if constexpr (kVecBytes == 16) v[u] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0);
+                    else if constexpr (kVecBytes == 4) v[u] = u2f(__builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, 0));
+                    else v[u] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const bool valid = j + (uint32_t)u < nval;
+                    const uint32_t id0 = (v0 + wbase + (j + (uint32_t)u) * 64u) * EPV;
+                    const uint32_t off = valid ? id0 - bm_base : 0u;
+                    const uint32_t aw = mask ? (s_allow[off >> 5] >> (off & 31u)) : 0xffffffffu;
+                    uint32_t pw = 0u;
+                    if constexpr (PEN != 0) pw = s_pen[off >> 5] >> (off & 31u);
+                    static_for<0, EPV>([&](auto E) __attribute__((always_inline)) {
+                        const uint32_t bits = VT::bits(v[u], E);
+                        const bool allowed = ((aw >> (int)E) & 1u) != 0u;
+                        uint32_t key;
+                        if ((pw >> (int)E) & 1u) {
+                            key = pen_key(bits, allowed, count_of(id0 + (uint32_t)E));
+                        } else {
+                            key = allowed ? raw_order_key(bits) : masked_key;
+                            key = key < valid_min ? 0u : key;
+                        }
+                        fn(valid ? key : 0u, id0 + (uint32_t)E);
+                    });
+                }
+            }
+            if (has_tail) {
+                const uint32_t off = tail_id - bm_base;
+                const bool allowed = !mask || ((s_allow[off >> 5] >> (off & 31u)) & 1u);
+                bool pen = false;
+                if constexpr (PEN != 0) pen = (s_pen[off >> 5] >> (off & 31u)) & 1u;
+                uint32_t key;
+                if (pen) {
+                    key = pen_key(tail_bits, allowed, count_of(tail_id));
+                } else {
+                    key = allowed ? raw_order_key(tail_bits) : masked_key;
+                    key = key < valid_min ? 0u : key;
+                }
+                fn(key, tail_id);
+            }
         };
         repad = true;
         uint32_t count_ge, G;
-        const uint32_t kv = radix_threshold_fn(tok0, tok1, k, sm.hist, sm.sel, count_ge, key_at, &G);
+        auto visit_keys = [&](auto &&fn) __attribute__((always_inline)) {
+            each_key([&](uint32_t key, uint32_t) __attribute__((always_inline)) { fn(key); });
+        };
+        const uint32_t kv = radix_threshold_visit(k, sm.hist, sm.sel, count_ge, visit_keys, &G);
         // G keys above kv; `need` of the count_ge - G ties at kv qualify: all
         // of them when they fit, else the `need` smallest ids
         const uint32_t need = k > G ? k - G : 0u;
-        auto tie_at = [&](uint32_t tt) __attribute__((always_inline)) -> uint32_t { return key_at(tt) == kv ? ~tt : 0u; };
+        auto visit_ties = [&](auto &&fn) __attribute__((always_inline)) {
+            each_key([&](uint32_t key, uint32_t id) __attribute__((always_inline)) { fn(key == kv && key != 0u ? ~id : 0u); });
+        };
         uint32_t ties_ge;
         uint32_t id_cut = 0xffffffffu;
-        if (need && count_ge - G > need) id_cut = ~radix_threshold_fn(tok0, tok1, need, sm.hist, sm.sel, ties_ge, tie_at);
+        if (need && count_ge - G > need) id_cut = ~radix_threshold_visit(need, sm.hist, sm.sel, ties_ge, visit_ties);
         if (tid == 0) sm.flag[1] = 0u;
         lds_sync();
-        for (uint32_t t0c = tok0 + tid; t0c < tok1; t0c += 8u * kBlock) {
-            uint32_t keys[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const uint32_t tt = t0c + (uint32_t)u * kBlock;
-                keys[u] = tt < tok1 ? key_at(tt) : 0u;
+        each_key([&](uint32_t key, uint32_t id) __attribute__((always_inline)) {
+            if (key != 0u && (key > kv || (key == kv && need && id <= id_cut))) {
+                const uint32_t q = atomicAdd(&sm.flag[1], 1u);
+                if (q < kStreamCandCap) s_cand[q] = cand_pack(key, id);
             }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const uint32_t tt = t0c + (uint32_t)u * kBlock, key = keys[u];
-                if (key != 0u && (key > kv || (key == kv && need && tt <= id_cut))) {
-                    const uint32_t q = atomicAdd(&sm.flag[1], 1u);
-                    if (q < kStreamCandCap) s_cand[q] = cand_pack(key, tt);
-                }
-            }
-        }
+        });
         lds_sync();
         C = min(sm.flag[1], kStreamCandCap);
     }
