@@ -1543,9 +1543,13 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         auto visit_ties = [&](auto &&fn) __attribute__((always_inline)) {
             each_key([&](uint32_t key, uint32_t id) __attribute__((always_inline)) { fn(key == kv && key != 0u ? ~id : 0u); });
         };
+        // When every key >= kv fits the candidate list, all of them are
+        // collected and the rank sort orders the ties by id; otherwise the
+        // `need` smallest tie ids are found first (4 more passes).
         uint32_t ties_ge;
         uint32_t id_cut = 0xffffffffu;
-        if (need && count_ge - G > need) id_cut = ~radix_threshold_visit(need, sm.hist, sm.sel, ties_ge, visit_ties);
+        if (need && count_ge - G > need && count_ge > kStreamCandCap)
+            id_cut = ~radix_threshold_visit(need, sm.hist, sm.sel, ties_ge, visit_ties);
         if (tid == 0) sm.flag[1] = 0u;
         lds_sync();
         each_key([&](uint32_t key, uint32_t id) __attribute__((always_inline)) {
