@@ -238,3 +238,36 @@ def test_many_repeated_history_ids(oracle, dtype):
     ref = oracle.sample(logits, params, top_k_capacity=64, **kw)
     gpu = run_gpu(logits, params, top_k_capacity=64, **kw)
     assert_parity(gpu, ref, params, label="many-repeats", prob_rtol=1e-5 if dtype == "f32" else 2e-3)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("kcap", [64, 1024])
+def test_exact_path_with_ties_beyond_the_candidate_list(oracle, dtype, kcap):
+    """The 150 top raw logits of each row sit far above the rest and are all
+    penalised out of reach, so the slice falls back to the exact selection;
+    the remaining values are small integers, so thousands of tokens tie at
+    the k-th value and only the lowest ids among them may survive."""
+    from llmoop_amd.workloads import to_bf16_bits
+
+    rng = np.random.default_rng(73 + kcap)
+    B, V, H = 8, 40000, 256
+    x = rng.integers(-4, 4, size=(B, V)).astype(np.float32)
+    hist = np.zeros((B, H), np.uint32)
+    for r in range(B):
+        top = rng.choice(V, 150, replace=False)
+        x[r, top] = 10.0
+        hist[r, :150] = top
+        hist[r, 150:] = top[rng.integers(0, 150, H - 150)]
+    logits = to_bf16_bits(x) if dtype == "bf16" else x
+    params = _random_params(rng, B, kcap, method=1)
+    params["top_k"] = rng.integers(1, kcap + 1, B)
+    params["repetition_penalty"] = 50.0
+    params["frequency_penalty"] = 0.0
+    params["presence_penalty"] = 0.0
+    kw = dict(history=hist, history_len=np.full(B, H, np.uint32),
+              seeds=rng.integers(0, 2**32, B, dtype=np.uint64).astype(np.uint32),
+              steps=rng.integers(0, 2**40, B, dtype=np.uint64))
+    _say(f"exact path with ties {dtype} kcap={kcap}")
+    ref = oracle.sample(logits, params, top_k_capacity=kcap, **kw)
+    gpu = run_gpu(logits, params, top_k_capacity=kcap, **kw)
+    assert_parity(gpu, ref, params, label="exact-ties", prob_rtol=1e-5 if dtype == "f32" else 2e-3)
