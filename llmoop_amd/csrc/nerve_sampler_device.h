@@ -905,7 +905,7 @@ __host__ __device__ constexpr uint32_t slice_bitmap_words(uint32_t tokens, uint3
 // raw, so the raw test of pass 2 is conservative for penalised tokens too.
 // Other settings take penalised tokens out of the vector passes and evaluate
 // each one from the history state instead (one gather per id).
-template <typename Elem, int EPV, int NV, int PEN, bool MASK>
+template <typename Elem, int EPV, int NV, int PEN, bool MASK, int AUX>
 __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     constexpr int HPT = (kMaxHistory + kBlock - 1) / kBlock;  // history ids per lane
     constexpr int BW = (int)((slice_bitmap_words((uint32_t)kBlock * NV * EPV, EPV) + kBlock - 1u) / kBlock);
@@ -961,17 +961,12 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(lrow + (uint64_t)(v0 + wave * span) * EPV), (short)0, (int)(wslots * kVecBytes), 0x00020000);
     vec_t data[NV];
-    // cache policy of the stream's loads: NT (bit 1), since each logit is
-    // read once; it cut C5 from 20.65 to 19.7 us per step (sc0 or sc1 added
-    // to it changed nothing measurable)
-#ifndef NERVE_LOAD_AUX
-#define NERVE_LOAD_AUX 2
-#endif
+    // AUX: cache policy of the stream's loads (kLoadNT or 0)
     auto load = [&](int j) __attribute__((always_inline)) {
         const uint32_t off = (lane + (uint32_t)j * 64u) * kVecBytes;
-        if constexpr (kVecBytes == 16) data[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, NERVE_LOAD_AUX);
-        else if constexpr (kVecBytes == 4) data[j] = u2f(__builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, NERVE_LOAD_AUX));
-        else data[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, NERVE_LOAD_AUX);
+        if constexpr (kVecBytes == 16) data[j] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, AUX);
+        else if constexpr (kVecBytes == 4) data[j] = u2f(__builtin_amdgcn_raw_buffer_load_b32(rsrc, off, 0, AUX));
+        else data[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, AUX);
     };
     // lane-vectors in flight ahead of the one being processed
 #ifndef NERVE_LOOKAHEAD
@@ -1754,10 +1749,10 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
 // ---- launch ------------------------------------------------------------------
 
 
-template <typename Elem, int EPV, int NV, int PEN, bool MASK>
+template <typename Elem, int EPV, int NV, int PEN, bool MASK, int AUX>
 static hipError_t launch_one(const StepArgs &a0, hipStream_t stream) {
     StepArgs a = a0;
-    auto kern = sample_rows_kernel<Elem, EPV, NV, PEN, MASK>;
+    auto kern = sample_rows_kernel<Elem, EPV, NV, PEN, MASK, AUX>;
     hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                        (int)a.dyn_lds_bytes);
     if (e != hipSuccess) return e;
@@ -1774,11 +1769,25 @@ static hipError_t launch_one(const StepArgs &a0, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <typename Elem, int EPV, int NV, bool MASK>
+template <typename Elem, int EPV, int NV, bool MASK, int AUX = 0>
 static hipError_t launch_pen_mask(const StepArgs &a, hipStream_t stream) {
-    if (a.history) return launch_one<Elem, EPV, NV, 2, MASK>(a, stream);
-    if (a.seen) return launch_one<Elem, EPV, NV, 1, MASK>(a, stream);
-    return launch_one<Elem, EPV, NV, 0, MASK>(a, stream);
+    if (a.history) return launch_one<Elem, EPV, NV, 2, MASK, AUX>(a, stream);
+    if (a.seen) return launch_one<Elem, EPV, NV, 1, MASK, AUX>(a, stream);
+    return launch_one<Elem, EPV, NV, 0, MASK, AUX>(a, stream);
+}
+
+// Non-temporal (NT, bit 1) cache policy for the logits stream: each logit is
+// read once. It pays when the grid fills the chip (B=256 x V=151936 bf16:
+// 20.65 -> 19.7 us per step) and costs latency when it does not (B=64, same
+// V: 17.2 -> 18.2 us), so the long-row kernels are built both ways and the
+// launch picks by grid size. sc0 or sc1 added to NT changed nothing measurable.
+constexpr int kLoadNT = 2;
+constexpr uint32_t kNtMinGroups = 256;  // one workgroup per CU
+
+template <typename Elem, int EPV, int NV, bool MASK>
+static hipError_t launch_pen_mask_policy(const StepArgs &a, hipStream_t stream) {
+    if (a.batch * a.slices >= kNtMinGroups) return launch_pen_mask<Elem, EPV, NV, MASK, kLoadNT>(a, stream);
+    return launch_pen_mask<Elem, EPV, NV, MASK, 0>(a, stream);
 }
 
 
@@ -1794,9 +1803,9 @@ static hipError_t launch_vec(const StepArgs &a, hipStream_t stream) {
         case 8: return launch_pen_mask<Elem, EPV, 8, MASK>(a, stream);
         case 16: return launch_pen_mask<Elem, EPV, 16, MASK>(a, stream);
         case 24: return launch_pen_mask<Elem, EPV, 24, MASK>(a, stream);
-        case 32: return launch_pen_mask<Elem, EPV, 32, MASK>(a, stream);
+        case 32: return launch_pen_mask_policy<Elem, EPV, 32, MASK>(a, stream);
         case 40:
-            if constexpr (sizeof(Elem) == 2) return launch_pen_mask<Elem, EPV, 40, MASK>(a, stream);
+            if constexpr (sizeof(Elem) == 2) return launch_pen_mask_policy<Elem, EPV, 40, MASK>(a, stream);
             return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
