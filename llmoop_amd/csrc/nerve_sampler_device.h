@@ -970,7 +970,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     };
     // lane-vectors in flight ahead of the one being processed
 #ifndef NERVE_LOOKAHEAD
-#define NERVE_LOOKAHEAD 6
+#define NERVE_LOOKAHEAD 5
 #endif
     constexpr int D = NV < NERVE_LOOKAHEAD ? NV : NERVE_LOOKAHEAD;
     static_for<0, D>([&](auto J) __attribute__((always_inline)) { load(J); });
