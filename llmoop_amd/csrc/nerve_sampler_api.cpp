@@ -56,6 +56,7 @@ struct nerve_sampler {
     int device;
     uint32_t slices;           // requested workgroups per row (raised per step if the slice would not fit)
     uint32_t slices_capacity;  // scratch sized for this many
+    uint32_t last_slices;      // workgroups per row of the last step
     uint2 *scratch_lists;
     uint32_t *scratch_meta;
     size_t lds_per_block;      // hipDeviceProp_t::sharedMemPerBlock
@@ -215,6 +216,14 @@ int nerve_sampler_create(const nerve_sampler_desc *desc, nerve_sampler **out) {
     s->device = (int)d.device;
     s->slices = want;
     s->slices_capacity = capacity;
+    {
+        // before the first step: the count of an aligned step of this dtype
+        const uint32_t v = d.dtype == NERVE_DTYPE_F32 ? nerve::kVariantF32Vec : nerve::kVariantBf16Vec;
+        const uint32_t per = threads * nerve::max_vectors_per_lane(v);
+        const uint32_t nvec = d.vocab_size / nerve::elems_per_vector(v);
+        const uint32_t need_v = nvec ? (nvec + per - 1u) / per : 1u;
+        s->last_slices = want > need_v ? want : need_v;
+    }
     s->lds_per_block = prop.sharedMemPerBlock;
     int prev = 0;
     (void)hipGetDevice(&prev);
@@ -246,7 +255,7 @@ int nerve_sampler_destroy(nerve_sampler *s) {
     return NERVE_OK;
 }
 
-uint32_t nerve_sampler_slices_per_row(const nerve_sampler *s) { return s ? s->slices : 0u; }
+uint32_t nerve_sampler_slices_per_row(const nerve_sampler *s) { return s ? s->last_slices : 0u; }
 
 int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *stream) {
     if (!s || !b) return fail(NERVE_ERR_INVALID_ARGUMENT, "null argument");
@@ -334,6 +343,8 @@ int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *str
     const uint32_t stream_lds = nerve::stream_lds_bytes(variant, b->allowed != nullptr, pen, a.hash_slots,
                                                         a.bitmap_words, d.top_k_capacity);
     a.dyn_lds_bytes = stream_lds;
+    a.device = s->device;
+    s->last_slices = slices;
     const size_t static_lds = 2u * 1024u;  // reduction scratch
     if (stream_lds + static_lds > s->lds_per_block || a.finish_lds_bytes + static_lds > s->lds_per_block)
         return fail(NERVE_ERR_INVALID_ARGUMENT, "LDS need of this top_k_capacity / history / slice count exceeds the device");
@@ -373,8 +384,12 @@ int nerve_sampler_copy_token_state(nerve_sampler *s, uint32_t *dst, const uint32
                                    uint32_t seen_stride, void *stream) {
     if (!s || !dst || !src) return fail(NERVE_ERR_INVALID_ARGUMENT, "null argument");
     if (rows == 0u) return NERVE_OK;
+    int prev = 0;
+    (void)hipGetDevice(&prev);
+    if (prev != s->device) (void)hipSetDevice(s->device);
     hipError_t e = hipMemcpyAsync(dst, src, (size_t)rows * seen_stride * sizeof(uint32_t), hipMemcpyDeviceToDevice,
                                   (hipStream_t)stream);
+    if (prev != s->device) (void)hipSetDevice(prev);
     if (e != hipSuccess) return hip_fail(e, "copy_token_state");
     return NERVE_OK;
 }

@@ -36,6 +36,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <utility>
 
 #include "nerve_device_math.h"
@@ -43,24 +44,6 @@
 
 namespace nerve {
 
-#ifdef NERVE_PHASE_TIMING
-// Profiling builds only: per-workgroup shader-clock stamps at phase boundaries.
-__device__ uint64_t g_phase_ts[16384 * 16];
-#define PHASE_MARK(i)                                                                        \
-    do {                                                                                     \
-        if (threadIdx.x == 0 && blockIdx.x < 16384u)                                         \
-            g_phase_ts[blockIdx.x * 16u + (i)] = __builtin_amdgcn_s_memtime();               \
-    } while (0)
-__device__ uint32_t g_dbg[16384 * 4];
-#define DBG_ADD(i, v) atomicAdd(&g_dbg[blockIdx.x * 4u + (i)], (v))
-#define DBG_SET(i, v) (g_dbg[blockIdx.x * 4u + (i)] = (v))
-#else
-#define DBG_ADD(i, v) ((void)0)
-#define DBG_SET(i, v) ((void)0)
-#define PHASE_MARK(i) \
-    do {              \
-    } while (0)
-#endif
 
 constexpr int kBlock = 512;
 constexpr int kWaves = kBlock / 64;
@@ -591,21 +574,68 @@ struct RowIo {
     uint32_t seed, tick_lo, tick_hi, ring_cap;
 };
 
-__device__ __forceinline__ RowIo load_row_io(const StepArgs &a, uint32_t row) {
+// Per-row inputs are read with vector buffer loads: their completion is
+// tracked by the in-order vector-memory counter, so waiting for them never
+// waits for the logits issued after them (scalar or flat loads share a
+// counter with the kernel-argument loads and would be waited for before the
+// stream starts), and a null pointer becomes a zero-size buffer that reads 0
+// with no branch.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t small_rsrc(const void *p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc((void *)p, (short)0, p ? (int)bytes : 0, 0x00020000);
+}
+
+// The per-row inputs as issued at kernel start: lane i of each word holds
+// word i of its record, so nothing is uniform for the compiler to move into
+// scalar registers at once (which would wait for the loads before the logits
+// are issued); lane_word() takes the words out after the stream has started.
+struct RowLoads {
+    uint32_t params;  // lanes 0-7: nerve_sampler_row_params
+    uint32_t sc;      // lanes 0-4: stream control words
+    uint32_t steps;   // lanes 0-1: steps[row] (low, high)
+    uint32_t seed;    // lane 0
+    uint32_t hlen;    // lane 0: history_len[row]
+};
+
+__device__ __forceinline__ RowLoads issue_row_loads(const StepArgs &a, uint32_t row, uint32_t lane) {
+    RowLoads l;
+    const uint32_t w8 = (lane & 7u) * 4u, w2 = (lane & 1u) * 4u;
+    l.params = __builtin_amdgcn_raw_buffer_load_b32(small_rsrc(a.params + row, 32u), w8, 0, 0);
+    l.sc = __builtin_amdgcn_raw_buffer_load_b32(
+        small_rsrc(a.stream_control ? a.stream_control + (uint64_t)row * 5u : nullptr, 20u), w8, 0, 0);
+    l.steps = __builtin_amdgcn_raw_buffer_load_b32(small_rsrc(a.steps ? a.steps + row : nullptr, 8u), w2, 0, 0);
+    l.seed = __builtin_amdgcn_raw_buffer_load_b32(small_rsrc(a.seeds ? a.seeds + row : nullptr, 4u), w2, 0, 0);
+    l.hlen = __builtin_amdgcn_raw_buffer_load_b32(small_rsrc(a.history_len ? a.history_len + row : nullptr, 4u), w2, 0, 0);
+    return l;
+}
+
+__device__ __forceinline__ uint32_t lane_word(uint32_t v, int i) { return (uint32_t)__builtin_amdgcn_readlane((int)v, i); }
+
+__device__ __forceinline__ nerve_sampler_row_params row_params_of(const RowLoads &l) {
+    nerve_sampler_row_params p;
+    p.method = lane_word(l.params, 0);
+    p.temperature = u2f(lane_word(l.params, 1));
+    p.top_k = lane_word(l.params, 2);
+    p.top_p = u2f(lane_word(l.params, 3));
+    p.min_p = u2f(lane_word(l.params, 4));
+    p.repetition_penalty = u2f(lane_word(l.params, 5));
+    p.frequency_penalty = u2f(lane_word(l.params, 6));
+    p.presence_penalty = u2f(lane_word(l.params, 7));
+    return p;
+}
+
+// Draw inputs: the seed, the tick (stream control words 1-2, else the
+// step), and the output ring capacity (stream control word 4).
+__device__ __forceinline__ RowIo row_io_of(const StepArgs &a, const RowLoads &l) {
     RowIo io;
-    io.seed = a.seeds ? a.seeds[row] : 0u;
-    if (a.stream_control) {
-        const uint32_t *sc = a.stream_control + (uint64_t)row * 5u;
-        io.tick_lo = sc[1];
-        io.tick_hi = sc[2];
-        io.ring_cap = sc[4];
-    } else {
-        const uint64_t t = a.steps ? a.steps[row] : 0ull;
-        io.tick_lo = (uint32_t)t;
-        io.tick_hi = (uint32_t)(t >> 32);
-        io.ring_cap = 0u;
-    }
+    io.seed = lane_word(l.seed, 0);
+    io.tick_lo = a.stream_control ? lane_word(l.sc, 1) : lane_word(l.steps, 0);
+    io.tick_hi = a.stream_control ? lane_word(l.sc, 2) : lane_word(l.steps, 1);
+    io.ring_cap = lane_word(l.sc, 4);
     return io;
+}
+
+__device__ __forceinline__ RowIo load_row_io(const StepArgs &a, uint32_t row) {
+    return row_io_of(a, issue_row_loads(a, row, lane_id()));
 }
 
 // Finishes one row from its sorted survivors s_sorted[0 .. n) (value desc,
@@ -733,7 +763,6 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
             const float d = T * lg;
             minimum = l0 + d;
         }
-        PHASE_MARK(13);
         // The min-p cut (the first survivor below the floor ends the list),
         // then running sums in the reference's sequential order.
         uint32_t n_valid = k, nucleus, selected;
@@ -748,14 +777,12 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
             float w = 0.0f;
             if (lane < n_valid) w = nerve_expf(v / T - m);
             const float acc = sequential_prefix(w, 0.0f, n_valid);
-            PHASE_MARK(10);
             const float total = n_valid ? u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(n_valid - 1u))) : 0.0f;
             const float threshold = P.top_p * total;
             const uint64_t bn = __ballot(lane < n_valid && acc >= threshold);
             nucleus = bn ? (uint32_t)__builtin_ctzll(bn) + 1u : n_valid;
             if (nucleus == 0u) nucleus = 1u;
             nucleus_weight = n_valid ? u2f(__builtin_amdgcn_readlane(f2u(acc), (int)(nucleus - 1u))) : 0.0f;
-            PHASE_MARK(15);
             const float target = u * nucleus_weight;
             const uint64_t bs = __ballot(lane < nucleus && lane < n_valid && target < acc);
             selected = bs ? (uint32_t)__builtin_ctzll(bs) : nucleus - 1u;
@@ -813,7 +840,6 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
             token = e.y == kPadId ? kPadId : (e.y & kIdMask);
             sel_bits = f2u(entry_value(e));
         }
-        PHASE_MARK(11);
         out_flags = NERVE_FLAG_SAMPLED;
         kout = k;
     }
@@ -943,14 +969,14 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     const bool has_tail = last_slice && tail_id < a.vocab;
 
     const Elem *lrow = (const Elem *)a.logits + (uint64_t)row * a.ld;
-
-    PHASE_MARK(0);
-    // 1. loads: the first D lane-vectors first (they depend on the launch
-    // arguments only), through a buffer resource bounded by the wave's valid
-    // run; then the row parameters, history ids and bitmap words. A wave owns
-    // a run of consecutive slots, so the loads of a lane sit 64 slots apart
-    // and share one offset register per 4 KiB.
+    // 1. loads. The small per-row inputs first (parameters, draw inputs,
+    // history ids and the slice's bitmap words), so the set-up finds them
+    // landed, and without any wait before the logits are issued; then the
+    // first D lane-vectors through a buffer resource bounded by the wave's
+    // valid run. A wave owns a run of consecutive slots, so the loads of a
+    // lane sit 64 slots apart and share one offset register per 4 KiB.
     const uint32_t lane = lane_id();
+    const RowLoads rl = issue_row_loads(a, row, lane);
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     // the slice is spread evenly: wave w owns `span` slots from w * span
     const uint32_t span = ((a.vec_per_slice + (uint32_t)kBlock - 1u) / (uint32_t)kBlock) * 64u;
@@ -960,6 +986,29 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     // and costs no memory traffic
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(lrow + (uint64_t)(v0 + wave * span) * EPV), (short)0, (int)(wslots * kVecBytes), 0x00020000);
+    constexpr bool mask = MASK;  // an allowed-token bitmask is present
+    const uint32_t *arow = mask ? a.allowed + (uint64_t)row * a.allowed_stride : nullptr;
+    const uint32_t *srow = PEN == 1 ? a.seen + (uint64_t)row * a.seen_stride : nullptr;
+    uint32_t hist[history ? HPT : 1];
+    uint32_t hlen = 0;
+    if constexpr (history) {
+        const uint32_t *hrow = a.history + (uint64_t)row * a.history_stride;
+        const uint32_t hlast = a.history_stride - 1u;
+#pragma unroll
+        for (int h = 0; h < HPT; ++h) hist[h] = hrow[min(tid + (uint32_t)h * kBlock, hlast)];
+    }
+    const uint32_t bm_last = bm_n ? bm_n - 1u : 0u;
+    uint32_t mw[BW];
+    if (mask) {
+#pragma unroll
+        for (int i = 0; i < BW; ++i) mw[i] = arow[(bm_base >> 5) + min(tid + (uint32_t)i * kBlock, bm_last)];
+    }
+    uint32_t sw[PEN == 1 ? BW : 1];
+    if constexpr (PEN == 1) {
+#pragma unroll
+        for (int i = 0; i < BW; ++i) sw[i] = srow[(bm_base >> 5) + min(tid + (uint32_t)i * kBlock, bm_last)];
+    }
+
     vec_t data[NV];
     // AUX: cache policy of the stream's loads (kLoadNT or 0)
     auto load = [&](int j) __attribute__((always_inline)) {
@@ -975,40 +1024,15 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     constexpr int D = NV < NERVE_LOOKAHEAD ? NV : NERVE_LOOKAHEAD;
     static_for<0, D>([&](auto J) __attribute__((always_inline)) { load(J); });
 
-    const nerve_sampler_row_params P = a.params[row];
-    const RowIo io = a.slices == 1u ? load_row_io(a, row) : RowIo{0u, 0u, 0u, 0u};
+    const nerve_sampler_row_params P = row_params_of(rl);
+    const RowIo io = row_io_of(a, rl);
+    if constexpr (history) hlen = min(lane_word(rl.hlen, 0), a.history_stride);
     const bool sampled = P.method != NERVE_METHOD_GREEDY;
     uint32_t k = sampled ? P.top_k : 1u;
     k = k < 1u ? 1u : (k > a.kcap ? a.kcap : k);
     const uint32_t valid_min = sampled ? kMinFiniteKey : kNegInfKey;
     const uint32_t masked_key = sampled ? 0u : kNegInfKey;
-    constexpr bool mask = MASK;  // an allowed-token bitmask is present
     const bool lowering = P.repetition_penalty >= 1.0f && P.frequency_penalty >= 0.0f && P.presence_penalty >= 0.0f;
-
-    const uint32_t *arow = mask ? a.allowed + (uint64_t)row * a.allowed_stride : nullptr;
-    const uint32_t *srow = PEN == 1 ? a.seen + (uint64_t)row * a.seen_stride : nullptr;
-
-    uint32_t hist[history ? HPT : 1];
-    uint32_t hlen = 0;
-    if constexpr (history) {
-        const uint32_t *hrow = a.history + (uint64_t)row * a.history_stride;
-        const uint32_t hlast = a.history_stride - 1u;
-#pragma unroll
-        for (int h = 0; h < HPT; ++h) hist[h] = hrow[min(tid + (uint32_t)h * kBlock, hlast)];
-        hlen = min(a.history_len[row], a.history_stride);
-    }
-    const uint32_t bm_last = bm_n ? bm_n - 1u : 0u;
-    uint32_t mw[BW];
-    if (mask) {
-#pragma unroll
-        for (int i = 0; i < BW; ++i) mw[i] = arow[(bm_base >> 5) + min(tid + (uint32_t)i * kBlock, bm_last)];
-    }
-    uint32_t sw[PEN == 1 ? BW : 1];
-    if constexpr (PEN == 1) {
-#pragma unroll
-        for (int i = 0; i < BW; ++i) sw[i] = srow[(bm_base >> 5) + min(tid + (uint32_t)i * kBlock, bm_last)];
-    }
-    PHASE_MARK(1);
 
     // 2. LDS state: counters, mask / seen words of the slice (bits outside
     // [tok0, tok1) cleared); history ids -> bitmap, and repeats -> a table of
@@ -1082,7 +1106,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             }
         }
     };
-    PHASE_MARK(2);
 
     // 3. the stream. Lane-vector j is processed as it lands while lane-vector
     // j + D is issued. With a mask, per group of 8: the flags from the mask
@@ -1236,7 +1259,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     });
     set_thr(report_threshold(0));
     build_penalty_state();
-    PHASE_MARK(4);
     auto second_half = [&](auto fast_tag) __attribute__((always_inline)) {
         static_for<NA, NV>([&](auto J) __attribute__((always_inline)) {
             step_in(J);
@@ -1289,7 +1311,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         const uint32_t t = report_threshold(1);
         if (t > thr) set_thr(t);
     }
-    PHASE_MARK(5);
 
     // 5. exact keys of the staged elements (one lane per element), the tail,
     // and (for penalties that may raise a logit) every penalised token from
@@ -1424,7 +1445,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             }
         }
     }
-    PHASE_MARK(3);
     {
         // slice flags: bit 0 = some token allowed, bit 1 = greedy row holds a NaN
         const uint32_t f = (__ballot(any_allowed != 0u) ? 1u : 0u) | (__ballot(has_nan != 0u) ? 2u : 0u);
@@ -1452,7 +1472,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         push_staged();
         lds_sync();
     }
-    PHASE_MARK(6);
 
     RowCtx ctx;
     ctx.logits_row = lrow;
@@ -1467,15 +1486,8 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     ctx.pres = P.presence_penalty;
     ctx.history = history;
 
-    PHASE_MARK(7);
-
     // 7. selection -> s_sorted[0 .. n_out)
     uint32_t C = sm.flag[1];
-    if (tid == 0) {
-        DBG_SET(0, nstaged);
-        DBG_SET(1, C);
-        DBG_SET(2, thr);
-    }
     if (nstaged > kStageCap || C > kStreamCandCap || (C < k && thr > 1u)) {
         // Skewed slice (for example a constant row), or penalties that pushed
         // more than C - k of the reported values below thr: exact selection
@@ -1597,7 +1609,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     // rank sort (ids are distinct, so ranks are a permutation): G adjacent
     // lanes share a candidate, each counting the better entries in every G-th
     // position, and the partial ranks are summed across the group
-    PHASE_MARK(9);
     if (C <= kRankPad) {
         // The common case, unrolled: 8 adjacent lanes share a candidate (two,
         // i and i + 64, past 64 candidates), each comparing it with every 8th
@@ -1655,10 +1666,8 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         if (i < C && part == 0u && r < k) emit(r, cand_entry(e));
     }
     }
-    PHASE_MARK(14);
     const uint32_t n_out = C < k ? C : k;
     lds_sync();
-    PHASE_MARK(8);
 
 
     // 8. publish: with several slices the sorted list goes to scratch and the
@@ -1667,13 +1676,11 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         uint2 *lists = a.scratch_lists + (uint64_t)(row * a.slices + slice) * a.kcap;
         for (uint32_t i = tid; i < n_out; i += kBlock) lists[i] = s_sorted[i];
         if (tid == 0) a.scratch_meta[row * a.slices + slice] = n_out | (flags_slice << 16);
-        PHASE_MARK(12);
         return;
     }
     const RowIo io_l = {sm.io[0], sm.io[1], sm.io[2], sm.io[3]};
     finish_row<Elem, PEN, kBlock>(a, row, io_l, P, k, sampled, n_out, flags_slice, s_sorted, s_big, (float *)s_sslot,
                                   (float *)s_big + 64, s_hash, ctx, sm.u);
-    PHASE_MARK(12);
 }
 
 // Merges the S sorted slice lists of each row (one workgroup per row) and
@@ -1749,22 +1756,36 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
 // ---- launch ------------------------------------------------------------------
 
 
+constexpr int kMaxDevices = 64;
+
+// hipFuncSetAttribute(MaxDynamicSharedMemorySize) once per kernel, device and
+// size: the largest size set so far is remembered, so the hot launch makes no
+// attribute call.
+template <typename Kern>
+static hipError_t ensure_dyn_lds(Kern kern, int device, uint32_t bytes, std::atomic<uint32_t> (&done)[kMaxDevices]) {
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    if (done[device].load(std::memory_order_relaxed) >= bytes) return hipSuccess;
+    const hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e != hipSuccess) return e;
+    uint32_t prev = done[device].load(std::memory_order_relaxed);
+    while (prev < bytes && !done[device].compare_exchange_weak(prev, bytes)) {
+    }
+    return hipSuccess;
+}
+
 template <typename Elem, int EPV, int NV, int PEN, bool MASK, int AUX>
-static hipError_t launch_one(const StepArgs &a0, hipStream_t stream) {
-    StepArgs a = a0;
+static hipError_t launch_one(const StepArgs &a, hipStream_t stream) {
+    static std::atomic<uint32_t> rows_set[kMaxDevices];
+    static std::atomic<uint32_t> fin_set[kMaxDevices];
     auto kern = sample_rows_kernel<Elem, EPV, NV, PEN, MASK, AUX>;
-    hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)a.dyn_lds_bytes);
+    hipError_t e = ensure_dyn_lds(kern, a.device, a.dyn_lds_bytes, rows_set);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3(a.batch * a.slices), dim3(kBlock), a.dyn_lds_bytes, stream, a);
     e = hipGetLastError();
     if (e != hipSuccess || a.slices == 1u) return e;
     auto fin = finish_rows_kernel<Elem, PEN>;
-    if (a.finish_lds_bytes > 48u * 1024u) {
-        e = hipFuncSetAttribute((const void *)fin, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)a.finish_lds_bytes);
-        if (e != hipSuccess) return e;
-    }
+    e = ensure_dyn_lds(fin, a.device, a.finish_lds_bytes, fin_set);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(fin, dim3(a.batch), dim3(kFinishBlock), a.finish_lds_bytes, stream, a);
     return hipGetLastError();
 }

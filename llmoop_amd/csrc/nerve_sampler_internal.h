@@ -52,6 +52,7 @@ struct StepArgs {
     uint32_t big_entries;    // uint2 entries of the candidate / merge area
     uint32_t dyn_lds_bytes;     // slice kernel
     uint32_t finish_lds_bytes;  // finish kernel (slices > 1)
+    int device;                 // HIP ordinal the launch runs on
 };
 
 uint32_t elems_per_vector(uint32_t variant);

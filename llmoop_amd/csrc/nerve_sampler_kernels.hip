@@ -97,16 +97,3 @@ hipError_t launch_record_tokens(uint32_t *seen, uint32_t seen_stride, uint32_t r
 }
 
 }  // namespace nerve
-
-#ifdef NERVE_PHASE_TIMING
-extern "C" int nerve_debug_phase_ts(uint64_t *host, size_t count) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(nerve::g_phase_ts), count * sizeof(uint64_t));
-}
-extern "C" int nerve_debug_counters(uint32_t *host, size_t count) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(nerve::g_dbg), count * sizeof(uint32_t));
-}
-extern "C" int nerve_debug_clear(void) {
-    static uint32_t zeros[16384 * 4];
-    return (int)hipMemcpyToSymbol(HIP_SYMBOL(nerve::g_dbg), zeros, sizeof(zeros));
-}
-#endif
