@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define NERVE_SAMPLER_ABI_VERSION 1u
+#define NERVE_SAMPLER_ABI_VERSION 2u
 
 typedef enum {
     NERVE_OK = 0,
@@ -60,6 +60,35 @@ enum { NERVE_DTYPE_F32 = 0, NERVE_DTYPE_BF16 = 1 };
 enum { NERVE_METHOD_GREEDY = 0, NERVE_METHOD_TEMPERATURE_TOP_K_TOP_P = 1 };
 enum { NERVE_RNG_REFERENCE_HASH = 0, NERVE_RNG_PHILOX = 1 };
 enum { NERVE_FLAG_SAMPLED = 1u, NERVE_FLAG_EOS_FALLBACK = 2u };
+
+/* nerve_sampler_batch.flags */
+enum {
+    /* Append each row's sampled token to its penalty state after the step:
+     * history ids (count semantics): history[row][history_len[row] % history_stride] = token,
+     * history_len[row] += 1 (the rows then read the last history_stride ids);
+     * seen bitmap (set semantics): seen bit of the token set.
+     * Replaces the per-lane record_token_batch dispatch of the decode loop
+     * (multi_stream_batch_runner.rs:235-240; record_input_tokens, sampler.rs:773-814). */
+    NERVE_BATCH_APPEND_HISTORY = 1u,
+    /* The tick of row r is tick_base + r (steps and stream_control ignored for the tick):
+     * consecutive_component_batch_stream_ticks (stream_control_bytes.rs:54-67). */
+    NERVE_BATCH_CONSECUTIVE_TICKS = 2u
+};
+
+/* Feedback-control block (resident_feedback_control.rs:1-6, 397-424): words[0] flags
+ * (bit 0 enabled, bit 1 cancel requested), words[2] stop reason (0 none, 1 EOS,
+ * 2 cancelled), words[8] drain state, words[9] sampled ticks; the stop-token mask is
+ * its own array (the reference keeps it at word 12 of the same buffer). */
+enum { NERVE_FEEDBACK_ENABLED = 1u, NERVE_FEEDBACK_CANCEL_REQUESTED = 2u };
+enum { NERVE_STOP_REASON_NONE = 0u, NERVE_STOP_REASON_EOS = 1u, NERVE_STOP_REASON_CANCELLED = 2u };
+
+/* nerve_sampler_desc.flags */
+enum {
+    /* The handle allocates no device memory; steps whose rows need more than one
+     * slice (the only ones that use cross-workgroup scratch) must then go through
+     * nerve_sampler_step_static_scratch. */
+    NERVE_DESC_NO_SCRATCH = 1u
+};
 
 /* Up to this many token ids per row per record call
  * (VULKAN_BACKEND_LOOP_MAX_WINDOW, vulkan_stream_circuit.rs:82). */
@@ -126,7 +155,7 @@ typedef struct {
     uint32_t slices_per_row;    /* workgroups cooperating on one row; 0 = automatic: one, or the
                                    fewest whose registers hold the row (raised per step as needed) */
     uint32_t device;            /* HIP device ordinal */
-    uint32_t reserved;
+    uint32_t flags;             /* NERVE_DESC_* */
 } nerve_sampler_desc;
 
 /* Per-row sampling parameters (device array [batch], 32 bytes each). */
@@ -156,11 +185,11 @@ typedef struct {
     uint64_t logits_row_stride;            /* elements, >= vocab_size */
     const nerve_sampler_row_params *params;/* [batch] */
     /* Penalty state, at most one of: */
-    const uint32_t *history;               /* [batch][history_stride] token ids (count semantics) */
-    const uint32_t *history_len;           /* [batch] valid ids per row */
+    uint32_t *history;                     /* [batch][history_stride] token ids (count semantics) */
+    uint32_t *history_len;                 /* [batch] ids per row; the last min(len, history_stride) count */
     uint32_t history_stride;               /* <= history_capacity */
-    const uint32_t *seen;                  /* [batch][seen_stride] packed bitmap (set semantics) */
-    uint32_t seen_stride;                  /* words, >= ceil(V/32) */
+    uint32_t *seen;                        /* [batch][seen_stride] packed bitmap (set semantics) */
+    uint32_t seen_stride;                  /* words, >= ceil(V/32), or 0: one bitmap for all rows */
     /* Allowed-token bitmask (optional); an all-zero row samples eos_token_id. */
     const uint32_t *allowed;               /* [batch][allowed_stride] */
     uint32_t allowed_stride;
@@ -180,6 +209,26 @@ typedef struct {
     uint32_t *topk_ids;
     float *topk_logits;
     float *topk_probs;
+    /* ---- ABI 2 ---- */
+    uint32_t flags;                        /* NERVE_BATCH_* */
+    uint32_t prefix_stride;                /* words between rows of prefix_ids (0: one list for all rows) */
+    uint64_t tick_base;                    /* with NERVE_BATCH_CONSECUTIVE_TICKS */
+    /* Per-lane token prefix added to the seen state (set semantics; requires seen): row r
+     * samples with seen[r] | {prefix_ids[r * prefix_stride + i] : i < count_r}, count_r =
+     * prefix_counts[r] (<= NERVE_TOKEN_BATCH_CAPACITY), or r + 1 when prefix_counts is null (the
+     * [..=r] prefixes of sample_batch, batched_output_projection.rs:277-298). seen_stride 0
+     * shares one base bitmap among all rows, like the lanes' copies of the runner's bitmap
+     * (prepare_token_state, sampler.rs:1146-1193); the seen arrays are not modified. */
+    const uint32_t *prefix_ids;
+    const uint32_t *prefix_counts;
+    /* Optional feedback-control commit of each row's token (commit_feedback_control,
+     * greedy_sampler_f32.comp.template:35-50): with words[0] bit 0 set, words[9] += 1; on a
+     * cancel request or a stop token, words[2] 0 -> 1 (EOS) or 2 (cancelled) by
+     * compare-and-swap, and words[8] = 2 by the row that won it. */
+    uint32_t *feedback_control;            /* [batch][feedback_stride] words (stride 0: one shared block) */
+    const uint32_t *stop_tokens;           /* [batch][stop_stride] packed bitmask (stride 0: one mask) */
+    uint32_t feedback_stride;
+    uint32_t stop_stride;
 } nerve_sampler_batch;
 
 int nerve_sampler_create(const nerve_sampler_desc *desc, nerve_sampler **out);

@@ -272,7 +272,22 @@ int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *str
         if (b->history_stride == 0u || b->history_stride > d.history_capacity)
             return fail(NERVE_ERR_HISTORY_CAPACITY_OVERFLOW, "history_stride must be in 1..history_capacity");
     }
-    if (b->seen && b->seen_stride < words) return fail(NERVE_ERR_INVALID_ARGUMENT, "seen_stride < ceil(vocab/32)");
+    if (b->seen && b->seen_stride != 0u && b->seen_stride < words)
+        return fail(NERVE_ERR_INVALID_ARGUMENT, "seen_stride must be 0 (one shared bitmap) or >= ceil(vocab/32)");
+    if (b->flags & ~(uint32_t)(NERVE_BATCH_APPEND_HISTORY | NERVE_BATCH_CONSECUTIVE_TICKS))
+        return fail(NERVE_ERR_INVALID_ARGUMENT, "unknown batch flags");
+    if ((b->flags & NERVE_BATCH_APPEND_HISTORY) && !b->history && !b->seen)
+        return fail(NERVE_ERR_INVALID_ARGUMENT, "NERVE_BATCH_APPEND_HISTORY needs a history list or a seen bitmap");
+    if (b->prefix_ids && !b->seen)
+        return fail(NERVE_ERR_INVALID_ARGUMENT, "prefix_ids extend a seen bitmap (set semantics)");
+    if (b->prefix_ids && !b->prefix_counts && b->batch > NERVE_TOKEN_BATCH_CAPACITY) {
+        char buf[128];
+        std::snprintf(buf, sizeof(buf), "sampler repetition-state batch requests %u tokens, capacity is %u", b->batch,
+                      NERVE_TOKEN_BATCH_CAPACITY);
+        return fail(NERVE_ERR_TOKEN_BATCH_CAPACITY_EXCEEDED, buf);
+    }
+    if (b->stop_tokens && !b->feedback_control)
+        return fail(NERVE_ERR_INVALID_ARGUMENT, "stop_tokens need a feedback_control block");
     if (b->allowed && b->allowed_stride < words) return fail(NERVE_ERR_INVALID_ARGUMENT, "allowed_stride < ceil(vocab/32)");
     if (b->output_ring && !b->stream_control) return fail(NERVE_ERR_INVALID_ARGUMENT, "output_ring requires stream_control");
     if (b->output_ring && b->ring_stride < 4u) return fail(NERVE_ERR_INVALID_ARGUMENT, "ring_stride must hold the 4-word record");
@@ -344,6 +359,15 @@ int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *str
                                                         a.bitmap_words, d.top_k_capacity);
     a.dyn_lds_bytes = stream_lds;
     a.device = s->device;
+    a.flags = b->flags;
+    a.tick_base = b->tick_base;
+    a.prefix_ids = b->prefix_ids;
+    a.prefix_counts = b->prefix_counts;
+    a.prefix_stride = b->prefix_stride;
+    a.feedback_control = b->feedback_control;
+    a.feedback_stride = b->feedback_stride;
+    a.stop_tokens = b->stop_tokens;
+    a.stop_stride = b->stop_stride;
     s->last_slices = slices;
     const size_t static_lds = 2u * 1024u;  // reduction scratch
     if (stream_lds + static_lds > s->lds_per_block || a.finish_lds_bytes + static_lds > s->lds_per_block)

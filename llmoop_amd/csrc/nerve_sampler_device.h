@@ -357,6 +357,14 @@ struct VecTraits<uint16_t, 1> {
     __device__ static __forceinline__ uint32_t bits_dyn(const load_t &r, uint32_t) { return (uint32_t)r << 16; }
 };
 
+// Tokens of row `row`'s seen-state prefix: prefix_counts[row] (at most the
+// token-batch capacity), or row + 1 for the [..=row] prefixes of a batch.
+__device__ __forceinline__ uint32_t prefix_count(const StepArgs &a, uint32_t row) {
+    if (!a.prefix_ids) return 0u;
+    const uint32_t n = a.prefix_counts ? a.prefix_counts[row] : row + 1u;
+    return n < NERVE_TOKEN_BATCH_CAPACITY ? n : NERVE_TOKEN_BATCH_CAPACITY;
+}
+
 // Row state shared by the helpers that recompute a single configured value.
 struct RowCtx {
     const void *logits_row;
@@ -370,6 +378,8 @@ struct RowCtx {
     uint32_t tok0;
     float rep, freq, pres;
     bool history;
+    const uint32_t *prefix;  // seen-state prefix of the row (set semantics), prefix_n ids
+    uint32_t prefix_n;
 };
 
 template <typename Elem>
@@ -384,8 +394,13 @@ __device__ __forceinline__ float configured_at(const RowCtx &c, uint32_t t) {
         } else {
             count = hash_lookup(c.hash, c.log2_slots, t);
         }
+    } else if (c.bitmap) {
+        // the slice's LDS copy of the seen words, prefix included
+        const uint32_t o = t - c.tok0;
+        count = (c.bitmap[o >> 5] >> (o & 31u)) & 1u;
     } else if (c.seen_row) {
         count = (c.seen_row[t >> 5] >> (t & 31u)) & 1u;
+        for (uint32_t i = 0; i < c.prefix_n && count == 0u; ++i) count = c.prefix[i] == t ? 1u : 0u;
     }
     return configured_logit(x, allowed, count, c.rep, c.freq, c.pres);
 }
@@ -625,17 +640,23 @@ __device__ __forceinline__ nerve_sampler_row_params row_params_of(const RowLoads
 
 // Draw inputs: the seed, the tick (stream control words 1-2, else the
 // step), and the output ring capacity (stream control word 4).
-__device__ __forceinline__ RowIo row_io_of(const StepArgs &a, const RowLoads &l) {
+__device__ __forceinline__ RowIo row_io_of(const StepArgs &a, const RowLoads &l, uint32_t row) {
     RowIo io;
     io.seed = lane_word(l.seed, 0);
     io.tick_lo = a.stream_control ? lane_word(l.sc, 1) : lane_word(l.steps, 0);
     io.tick_hi = a.stream_control ? lane_word(l.sc, 2) : lane_word(l.steps, 1);
+    if (a.flags & NERVE_BATCH_CONSECUTIVE_TICKS) {
+        // consecutive ticks of sample_batch: tick_base + row
+        const uint64_t t = a.tick_base + row;
+        io.tick_lo = (uint32_t)t;
+        io.tick_hi = (uint32_t)(t >> 32);
+    }
     io.ring_cap = lane_word(l.sc, 4);
     return io;
 }
 
 __device__ __forceinline__ RowIo load_row_io(const StepArgs &a, uint32_t row) {
-    return row_io_of(a, issue_row_loads(a, row, lane_id()));
+    return row_io_of(a, issue_row_loads(a, row, lane_id()), row);
 }
 
 // Finishes one row from its sorted survivors s_sorted[0 .. n) (value desc,
@@ -869,6 +890,31 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
             if (next == 0u) sc[2] = io.tick_hi + 1u;
             sc[1] = next;
         }
+        if ((a.flags & NERVE_BATCH_APPEND_HISTORY) && token < a.vocab) {
+            // the sampled token joins the row's penalty state for the next step
+            if (a.history) {
+                const uint32_t len = a.history_len[row];
+                a.history[(uint64_t)row * a.history_stride + len % a.history_stride] = token;
+                a.history_len[row] = len + 1u;
+            } else if (a.seen) {
+                atomicOr(&a.seen[(uint64_t)row * a.seen_stride + (token >> 5)], 1u << (token & 31u));
+            }
+        }
+        if (a.feedback_control) {
+            // commit_feedback_control (greedy_sampler_f32.comp.template:35-50)
+            uint32_t *fc = a.feedback_control + (uint64_t)row * a.feedback_stride;
+            const uint32_t fl = __hip_atomic_load(&fc[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (fl & NERVE_FEEDBACK_ENABLED) {
+                atomicAdd(&fc[9], 1u);
+                const bool cancelled = (fl & NERVE_FEEDBACK_CANCEL_REQUESTED) != 0u;
+                const uint32_t *stop = a.stop_tokens ? a.stop_tokens + (uint64_t)row * a.stop_stride : nullptr;
+                const bool eos = stop && token < a.vocab && ((stop[token >> 5] >> (token & 31u)) & 1u);
+                if (cancelled || eos) {
+                    if (atomicCAS(&fc[2], 0u, cancelled ? NERVE_STOP_REASON_CANCELLED : NERVE_STOP_REASON_EOS) == 0u)
+                        __hip_atomic_store(&fc[8], 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+        }
     }
     if (a.topk_ids || a.topk_logits || a.topk_probs) {
         if (sampled && !eos) kout = k;  // set by wave 0 only
@@ -1004,9 +1050,11 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         for (int i = 0; i < BW; ++i) mw[i] = arow[(bm_base >> 5) + min(tid + (uint32_t)i * kBlock, bm_last)];
     }
     uint32_t sw[PEN == 1 ? BW : 1];
+    uint32_t pid = 0xffffffffu;  // seen-state prefix token of this lane (wave 0), if any
     if constexpr (PEN == 1) {
 #pragma unroll
         for (int i = 0; i < BW; ++i) sw[i] = srow[(bm_base >> 5) + min(tid + (uint32_t)i * kBlock, bm_last)];
+        if (a.prefix_ids && tid < prefix_count(a, row)) pid = a.prefix_ids[(uint64_t)row * a.prefix_stride + tid];
     }
 
     vec_t data[NV];
@@ -1025,7 +1073,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     static_for<0, D>([&](auto J) __attribute__((always_inline)) { load(J); });
 
     const nerve_sampler_row_params P = row_params_of(rl);
-    const RowIo io = row_io_of(a, rl);
+    const RowIo io = row_io_of(a, rl, row);
     if constexpr (history) hlen = min(lane_word(rl.hlen, 0), a.history_stride);
     const bool sampled = P.method != NERVE_METHOD_GREEDY;
     uint32_t k = sampled ? P.top_k : 1u;
@@ -1091,6 +1139,12 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             for (int i = 0; i < BW; ++i) {
                 const uint32_t w = tid + (uint32_t)i * kBlock;
                 if (w < bm_n) s_pen[w] = sw[i] & range_bits(w);
+            }
+            if (a.prefix_ids) {
+                // the lane's prefix token, after every word is stored (the
+                // barrier before the exact pass makes it visible)
+                lds_sync();
+                if (pid >= tok0 && pid < tok1) atomicOr(&s_pen[(pid - bm_base) >> 5], 1u << ((pid - bm_base) & 31u));
             }
         }
     };
@@ -1478,13 +1532,15 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     ctx.allowed_row = arow;
     ctx.seen_row = srow;
     ctx.hash = s_hash;
-    ctx.bitmap = s_pen;
+    ctx.bitmap = PEN != 0 ? s_pen : nullptr;
     ctx.log2_slots = a.log2_slots;
     ctx.tok0 = bm_base;
     ctx.rep = P.repetition_penalty;
     ctx.freq = P.frequency_penalty;
     ctx.pres = P.presence_penalty;
     ctx.history = history;
+    ctx.prefix = PEN == 1 && a.prefix_ids ? a.prefix_ids + (uint64_t)row * a.prefix_stride : nullptr;
+    ctx.prefix_n = PEN == 1 ? prefix_count(a, row) : 0u;
 
     // 7. selection -> s_sorted[0 .. n_out)
     uint32_t C = sm.flag[1];
@@ -1749,6 +1805,8 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
     ctx.freq = P.frequency_penalty;
     ctx.pres = P.presence_penalty;
     ctx.history = PEN == 2;
+    ctx.prefix = PEN == 1 && a.prefix_ids ? a.prefix_ids + (uint64_t)row * a.prefix_stride : nullptr;
+    ctx.prefix_n = PEN == 1 ? prefix_count(a, row) : 0u;
     finish_row<Elem, PEN, kFinishBlock>(a, row, io, P, k, sampled, n, row_flags, s_sorted, s_big, s_wt, (float *)s_big,
                                         s_hash, ctx, u);
 }

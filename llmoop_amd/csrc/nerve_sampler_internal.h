@@ -19,10 +19,10 @@ struct StepArgs {
     const void *logits;
     uint64_t ld;
     const nerve_sampler_row_params *params;
-    const uint32_t *history;
-    const uint32_t *history_len;
+    uint32_t *history;
+    uint32_t *history_len;
     uint32_t history_stride;
-    const uint32_t *seen;
+    uint32_t *seen;
     uint32_t seen_stride;
     const uint32_t *allowed;
     uint32_t allowed_stride;
@@ -53,6 +53,15 @@ struct StepArgs {
     uint32_t dyn_lds_bytes;     // slice kernel
     uint32_t finish_lds_bytes;  // finish kernel (slices > 1)
     int device;                 // HIP ordinal the launch runs on
+    uint32_t flags;             // NERVE_BATCH_*
+    uint64_t tick_base;
+    const uint32_t *prefix_ids;
+    const uint32_t *prefix_counts;
+    uint32_t prefix_stride;
+    uint32_t *feedback_control;
+    uint32_t feedback_stride;
+    const uint32_t *stop_tokens;
+    uint32_t stop_stride;
 };
 
 uint32_t elems_per_vector(uint32_t variant);

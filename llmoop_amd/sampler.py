@@ -42,6 +42,15 @@ RNG_REFERENCE_HASH = 0
 RNG_PHILOX = 1
 FLAG_SAMPLED = 1
 FLAG_EOS_FALLBACK = 2
+BATCH_APPEND_HISTORY = 1
+BATCH_CONSECUTIVE_TICKS = 2
+FEEDBACK_ENABLED = 1
+FEEDBACK_CANCEL_REQUESTED = 2
+STOP_REASON_NONE = 0
+STOP_REASON_EOS = 1
+STOP_REASON_CANCELLED = 2
+FEEDBACK_HEADER_WORDS = 12
+DESC_NO_SCRATCH = 1
 TOKEN_BATCH_CAPACITY = 64
 PAD_ID = 0xFFFFFFFF
 
@@ -111,7 +120,7 @@ class _Desc(ctypes.Structure):
         ("history_capacity", ctypes.c_uint32),
         ("slices_per_row", ctypes.c_uint32),
         ("device", ctypes.c_uint32),
-        ("reserved", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32),
     ]
 
 
@@ -139,6 +148,15 @@ class _Batch(ctypes.Structure):
         ("topk_ids", ctypes.c_void_p),
         ("topk_logits", ctypes.c_void_p),
         ("topk_probs", ctypes.c_void_p),
+        ("flags", ctypes.c_uint32),
+        ("prefix_stride", ctypes.c_uint32),
+        ("tick_base", ctypes.c_uint64),
+        ("prefix_ids", ctypes.c_void_p),
+        ("prefix_counts", ctypes.c_void_p),
+        ("feedback_control", ctypes.c_void_p),
+        ("stop_tokens", ctypes.c_void_p),
+        ("feedback_stride", ctypes.c_uint32),
+        ("stop_stride", ctypes.c_uint32),
     ]
 
 
@@ -348,12 +366,17 @@ class Sampler:
 
     def step(self, logits, params, out, *, history=None, history_len=None, seen=None, allowed=None,
              eos_token_id: int = 2, seeds=None, steps=None, rng: int = RNG_REFERENCE_HASH, stream_control=None,
-             output_ring=None, topk_ids=None, topk_logits=None, topk_probs=None, stream=None) -> None:
+             output_ring=None, topk_ids=None, topk_logits=None, topk_probs=None, stream=None, flags: int = 0,
+             tick_base: int = 0, seen_shared: bool = False, prefix_ids=None, prefix_counts=None,
+             feedback_control=None, stop_tokens=None, entry: str = "nerve_sampler_step") -> None:
         """Launches one step. All array arguments are torch tensors on the device:
         logits [B, stride] (float32, or bfloat16/int16 bits), params uint8 [B*32] holding ROW_PARAMS records,
-        out int32 [B, 4], optional history int32 [B, H] + history_len int32 [B], seen / allowed int32 [B, W],
-        seeds int32 [B], steps int64 [B], stream_control int32 [B, 5], output_ring int32 [B, R],
-        topk_* [B, top_k_capacity]."""
+        out int32 [B, 4], optional history int32 [B, H] + history_len int32 [B], seen / allowed int32 [B, W]
+        (seen [1, W] with seen_shared: one bitmap for every row), seeds int32 [B], steps int64 [B],
+        stream_control int32 [B, 5], output_ring int32 [B, R], topk_* [B, top_k_capacity];
+        prefix_ids int32 [B, P] with prefix_counts int32 [B], or [n] without counts (row r takes ids[:r+1]);
+        feedback_control int32 [B, F] or [F] (one block for every row), stop_tokens int32 [B, W] or [W].
+        `entry` selects the C entry point (nerve_sampler_step or nerve_sampler_step_static_scratch)."""
         b = _Batch()
         logits, lstride = _rows(logits)
         B = logits.shape[0]
@@ -369,6 +392,8 @@ class Sampler:
         if seen is not None:
             seen, b.seen_stride = _rows(seen)
             b.seen = seen.data_ptr()
+            if seen_shared:
+                b.seen_stride = 0
         if allowed is not None:
             allowed, b.allowed_stride = _rows(allowed)
             b.allowed = allowed.data_ptr()
@@ -385,7 +410,24 @@ class Sampler:
         b.topk_ids = _ptr(topk_ids)
         b.topk_logits = _ptr(topk_logits)
         b.topk_probs = _ptr(topk_probs)
-        _check(load_library().nerve_sampler_step(self._h, ctypes.byref(b), _stream_arg(stream, self.device)))
+        b.flags = flags
+        b.tick_base = tick_base
+        if prefix_ids is not None:
+            if prefix_ids.dim() == 1:
+                b.prefix_stride = 0
+            else:
+                prefix_ids, b.prefix_stride = _rows(prefix_ids)
+            b.prefix_ids = prefix_ids.data_ptr()
+            b.prefix_counts = _ptr(prefix_counts)
+        if feedback_control is not None:
+            if not feedback_control.is_contiguous():
+                raise ValueError("feedback_control must be contiguous (it is written in place)")
+            b.feedback_control = feedback_control.data_ptr()
+            b.feedback_stride = 0 if feedback_control.dim() == 1 else feedback_control.shape[1]
+        if stop_tokens is not None:
+            b.stop_tokens = stop_tokens.data_ptr()
+            b.stop_stride = 0 if stop_tokens.dim() == 1 else _rows(stop_tokens)[1]
+        _check(getattr(load_library(), entry)(self._h, ctypes.byref(b), _stream_arg(stream, self.device)))
 
     def record_tokens(self, seen, ids, counts, max_count: int, stream=None) -> None:
         """seen int32 [rows, W]; ids int32 [rows, n]; counts int32 [rows] (device)."""
@@ -540,44 +582,57 @@ class SamplerRunner:
     def restore_token_state(self) -> None:
         self.sampler.copy_token_state(self.seen, self.snapshot)
 
-    def sample_lanes(self, logits, token_prefixes, stream_ticks, dynamic_state_capacities=None) -> list[SamplerRun]:
-        """Per-lane views over a [B, V] logits buffer: each lane copies the
-        runner's seen state, adds its prefix tokens, samples at its own tick,
-        and writes the runner's ring slot for that tick."""
+    def sample_lanes(self, logits, token_prefixes, stream_ticks, dynamic_state_capacities=None, *,
+                     consecutive_from: int | None = None) -> list[SamplerRun]:
+        """Per-lane views over a [B, V] logits buffer (batched_output_projection.rs:316-371): lane i
+        samples with the runner's seen state plus its prefix tokens (added on the device by the step
+        itself, the runner's bitmap shared by every lane and left unchanged), at its own tick, and
+        writes the runner's ring slot for that tick. One launch; one device-to-host copy of B records."""
         torch = self.torch
         B = len(token_prefixes)
         if B == 0 or B > self.sampler.max_batch:
             raise SamplerError(ERR_BATCH_CAPACITY_EXCEEDED, f"cannot sample {B} lanes")
-        seen = self.seen.expand(B, -1).contiguous()
+        if len(stream_ticks) != B:
+            raise SamplerError(ERR_INVALID_ARGUMENT, f"{B} token lanes and {len(stream_ticks)} stream ticks")
+        kw = {}
         if self.token_state_active:
             n = max((len(p) for p in token_prefixes), default=0)
             if n > TOKEN_BATCH_CAPACITY:
-                raise SamplerError(ERR_TOKEN_BATCH_CAPACITY_EXCEEDED, "prefix exceeds the token batch capacity")
+                raise SamplerError(ERR_TOKEN_BATCH_CAPACITY_EXCEEDED,
+                                   f"sampler repetition-state batch requests {n} tokens, capacity is {TOKEN_BATCH_CAPACITY}")
+            kw["seen"] = self.seen
+            kw["seen_shared"] = True
             if n:
                 ids = np.zeros((B, n), np.uint32)
                 counts = np.zeros(B, np.int32)
                 for i, p in enumerate(token_prefixes):
                     ids[i, :len(p)] = p
                     counts[i] = len(p)
-                self.sampler.record_tokens(seen, torch.from_numpy(ids.view(np.int32)).to(self.device),
-                                           torch.from_numpy(counts).to(self.device), n)
-        sc = torch.zeros((B, 5), dtype=torch.int32, device=self.device)
-        caps = dynamic_state_capacities or [self.history_capacity] * B
+                kw["prefix_ids"] = torch.from_numpy(ids.view(np.int32)).to(self.device)
+                kw["prefix_counts"] = torch.from_numpy(counts).to(self.device)
+        caps = list(dynamic_state_capacities or [self.history_capacity] * B)
         scn = np.zeros((B, 5), np.uint32)
         for i, t in enumerate(stream_ticks):
             scn[i, 1] = t & 0xFFFFFFFF
             scn[i, 2] = t >> 32
             scn[i, 4] = caps[i]
-        sc.copy_(torch.from_numpy(scn.view(np.int32)))
+        sc = torch.from_numpy(scn.view(np.int32)).to(self.device)
         ring = torch.zeros((B, self.ring.shape[1]), dtype=torch.int32, device=self.device)
         out = torch.zeros((B, 4), dtype=torch.int32, device=self.device)
-        self.sampler.step(logits, self.params[: B * 32], out, seen=seen if self.token_state_active else None,
-                          seeds=self.seeds[:B], rng=RNG_REFERENCE_HASH, stream_control=sc, output_ring=ring)
-        ringn = ring.cpu().numpy().view(np.uint32)
-        runs = []
-        for i, t in enumerate(stream_ticks):
-            slot = (t & 0xFFFFFFFF) % caps[i]
-            rec = ringn[i, 4 + 4 * slot: 8 + 4 * slot]
-            self.ring[0, 4 + 4 * slot: 8 + 4 * slot] = torch.from_numpy(rec.view(np.int32).copy()).to(self.device)
-            runs.append(SamplerRun(self.spec.sampler_id, int(rec[0]), int(rec[1]), int(rec[2])))
-        return runs
+        self.sampler.step(logits, self.params[: B * 32], out, seeds=self.seeds[:B], rng=RNG_REFERENCE_HASH,
+                          stream_control=sc, output_ring=ring, **kw)
+        slots = np.array([(t & 0xFFFFFFFF) % c for t, c in zip(stream_ticks, caps)], np.int64)
+        cols = torch.from_numpy(4 + 4 * slots[:, None] + np.arange(4)[None, :]).to(self.device)
+        recs = torch.gather(ring, 1, cols)  # [B, 4] ring records of each lane's tick
+        self.ring[0].scatter_(0, cols.reshape(-1), recs.reshape(-1))
+        recn = recs.cpu().numpy().view(np.uint32)
+        return [SamplerRun(self.spec.sampler_id, int(r[0]), int(r[1]), int(r[2])) for r in recn]
+
+    def sample_batch(self, logits, input_token_ids, start_stream_tick: int,
+                     dynamic_state_capacity_activations: int | None = None) -> list[SamplerRun]:
+        """sample_batch (batched_output_projection.rs:277-298): lane i samples with the prefix
+        input_token_ids[..=i] at tick start + i (speculative verification of a drafted window)."""
+        n = len(input_token_ids)
+        cap = self.history_capacity if dynamic_state_capacity_activations is None else dynamic_state_capacity_activations
+        ticks = [start_stream_tick + i for i in range(n)]
+        return self.sample_lanes(logits, [list(input_token_ids[: i + 1]) for i in range(n)], ticks, [cap] * n)

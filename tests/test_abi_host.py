@@ -27,7 +27,35 @@ def test_header_symbols_are_exported(S):
     lib = S.load_library()
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.nerve_sampler_abi_version() == 1
+    assert lib.nerve_sampler_abi_version() == 2
+
+
+def test_ctypes_structs_match_the_header(S, tmp_path):
+    """The Python binding's struct layouts equal the C header's (offsets from a
+    host program compiled against include/nerve_sampler.h)."""
+    import ctypes
+    import subprocess
+
+    structs = {"nerve_sampler_batch": S._Batch, "nerve_sampler_desc": S._Desc,
+               "nerve_sampler_spec": S._Spec, "nerve_sampler_runtime_config": S._RuntimeConfig}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "nerve_sampler.h"', "int main(void) {"]
+    for cname, cls in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.splitlines():
+        cname, field, value = line.split()
+        got[(cname, field)] = int(value)
+    for cname, cls in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(cls), cname
+        for fname, _ in cls._fields_:
+            assert got[(cname, fname)] == getattr(cls, fname).offset, (cname, fname)
 
 
 def test_runtime_override_promotes_greedy(S):
