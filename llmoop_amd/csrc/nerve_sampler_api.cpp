@@ -230,9 +230,11 @@ int nerve_sampler_create(const nerve_sampler_desc *desc, nerve_sampler **out) {
     (void)hipSetDevice(s->device);
     const size_t lists_bytes = (size_t)d.max_batch * capacity * d.top_k_capacity * sizeof(uint2);
     const size_t meta_bytes = (size_t)d.max_batch * capacity * sizeof(uint32_t);
-    e = hipMalloc((void **)&s->scratch_lists, lists_bytes);
-    if (e == hipSuccess) e = hipMalloc((void **)&s->scratch_meta, meta_bytes);
-    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (!(d.flags & NERVE_DESC_NO_SCRATCH)) {
+        e = hipMalloc((void **)&s->scratch_lists, lists_bytes);
+        if (e == hipSuccess) e = hipMalloc((void **)&s->scratch_meta, meta_bytes);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+    }
     (void)hipSetDevice(prev);
     if (e != hipSuccess) {
         int rc = hip_fail(e, "nerve_sampler_create scratch");
@@ -257,7 +259,12 @@ int nerve_sampler_destroy(nerve_sampler *s) {
 
 uint32_t nerve_sampler_slices_per_row(const nerve_sampler *s) { return s ? s->last_slices : 0u; }
 
-int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *stream) {
+namespace {
+
+// One step; `static_scratch` takes the cross-workgroup scratch (used only when
+// a row has several slices) from the library's static per-GPU array instead
+// of the handle's allocation.
+int step_impl(nerve_sampler *s, const nerve_sampler_batch *b, void *stream, bool static_scratch) {
     if (!s || !b) return fail(NERVE_ERR_INVALID_ARGUMENT, "null argument");
     const nerve_sampler_desc &d = s->desc;
     if (b->batch == 0u) return NERVE_OK;
@@ -376,10 +383,48 @@ int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *str
     int prev = 0;
     (void)hipGetDevice(&prev);
     if (prev != s->device) (void)hipSetDevice(s->device);
+    struct Restore {
+        int prev, dev;
+        ~Restore() {
+            if (prev != dev) (void)hipSetDevice(prev);
+        }
+    } restore{prev, s->device};
+    if (slices > 1u) {
+        const size_t lists = (size_t)b->batch * slices * d.top_k_capacity * sizeof(uint2);
+        const size_t meta = (size_t)b->batch * slices * sizeof(uint32_t);
+        if (static_scratch) {
+            if (lists + meta > nerve::kStaticScratchBytes) {
+                char buf[200];
+                std::snprintf(buf, sizeof(buf),
+                              "step needs %zu bytes of scratch (batch x slices x top_k_capacity), the static array "
+                              "holds %zu",
+                              lists + meta, nerve::kStaticScratchBytes);
+                return fail(NERVE_ERR_INVALID_ARGUMENT, buf);
+            }
+            void *base = nullptr;
+            const hipError_t e = nerve::static_scratch(s->device, &base);
+            if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+            a.scratch_lists = (uint2 *)base;
+            a.scratch_meta = (uint32_t *)((uint8_t *)base + lists);
+        } else if (!s->scratch_lists) {
+            return fail(NERVE_ERR_INVALID_ARGUMENT,
+                        "this handle was created with NERVE_DESC_NO_SCRATCH: steps with several slices per row go "
+                        "through nerve_sampler_step_static_scratch");
+        }
+    }
     hipError_t e = nerve::launch_sample_rows(variant, a, (hipStream_t)stream);
-    if (prev != s->device) (void)hipSetDevice(prev);
     if (e != hipSuccess) return hip_fail(e, "sample_rows launch");
     return NERVE_OK;
+}
+
+}  // namespace
+
+int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *stream) {
+    return step_impl(s, b, stream, false);
+}
+
+int nerve_sampler_step_static_scratch(nerve_sampler *s, const nerve_sampler_batch *b, void *stream) {
+    return step_impl(s, b, stream, true);
 }
 
 int nerve_sampler_record_tokens(nerve_sampler *s, uint32_t *seen, uint32_t seen_stride, uint32_t rows,

@@ -1814,8 +1814,6 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
 // ---- launch ------------------------------------------------------------------
 
 
-constexpr int kMaxDevices = 64;
-
 // hipFuncSetAttribute(MaxDynamicSharedMemorySize) once per kernel, device and
 // size: the largest size set so far is remembered, so the hot launch makes no
 // attribute call.

@@ -64,6 +64,15 @@ struct StepArgs {
     uint32_t stop_stride;
 };
 
+// Bytes of the static scratch array of nerve_sampler_step_static_scratch
+// (per GPU): slice lists of batch x slices x top_k_capacity entries of 8 bytes
+// plus 4 bytes of metadata per (row, slice).
+constexpr size_t kStaticScratchBytes = (size_t)4 << 20;
+constexpr int kMaxDevices = 64;
+// Device address of this GPU's static scratch array (the current device must
+// be `device`); taken once per device.
+hipError_t static_scratch(int device, void **ptr);
+
 uint32_t elems_per_vector(uint32_t variant);
 uint32_t block_threads();
 uint32_t merge_capacity();

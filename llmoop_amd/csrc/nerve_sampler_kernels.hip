@@ -1,9 +1,32 @@
 // nerve_sampler_kernels.hip -- launch dispatch, launch-shape helpers and the
 // seen-token recording kernel. The slice kernels are instantiated per variant
 // in nerve_rows_*.hip (device code in nerve_sampler_device.h).
+#include <mutex>
+
 #include "nerve_sampler_device.h"
 
 namespace nerve {
+
+// Cross-workgroup scratch of nerve_sampler_step_static_scratch: one array per
+// GPU, held until the process ends. In host code `scratch` names a host-side
+// stand-in, so launches use the device address hipGetSymbolAddress returns,
+// taken once per device with that device current.
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+hipError_t static_scratch(int device, void **ptr) {
+    static std::mutex mu;
+    static void *addr[kMaxDevices] = {};
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[device]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        addr[device] = p;
+    }
+    *ptr = addr[device];
+    return hipSuccess;
+}
 
 __global__ void record_tokens_kernel(uint32_t *seen, uint32_t seen_stride, uint32_t rows, const uint32_t *ids,
                                      uint32_t ids_stride, const uint32_t *counts, uint32_t max_count,

@@ -167,6 +167,7 @@ EXPORTED_SYMBOLS = (
     "nerve_sampler_create",
     "nerve_sampler_destroy",
     "nerve_sampler_step",
+    "nerve_sampler_step_static_scratch",
     "nerve_sampler_record_tokens",
     "nerve_sampler_copy_token_state",
     "nerve_sampler_last_error",
@@ -193,6 +194,7 @@ def load_library() -> ctypes.CDLL:
     lib.nerve_sampler_create.argtypes = [P, ctypes.POINTER(P)]
     lib.nerve_sampler_destroy.argtypes = [P]
     lib.nerve_sampler_step.argtypes = [P, P, P]
+    lib.nerve_sampler_step_static_scratch.argtypes = [P, P, P]
     lib.nerve_sampler_record_tokens.argtypes = [P, P, u32, u32, P, u32, P, u32, P]
     lib.nerve_sampler_copy_token_state.argtypes = [P, P, P, u32, u32, P]
     lib.nerve_sampler_last_error.restype = ctypes.c_char_p
@@ -329,7 +331,7 @@ class Sampler:
     """One handle of the batched device sampler (nerve_sampler_create)."""
 
     def __init__(self, vocab_size: int, max_batch: int, *, dtype: str = "f32", top_k_capacity: int = 64,
-                 history_capacity: int = 0, slices_per_row: int = 0, device: int = 0):
+                 history_capacity: int = 0, slices_per_row: int = 0, device: int = 0, flags: int = 0):
         lib = load_library()
         d = _Desc()
         d.vocab_size = vocab_size
@@ -339,6 +341,7 @@ class Sampler:
         d.history_capacity = history_capacity
         d.slices_per_row = slices_per_row
         d.device = device
+        d.flags = flags
         h = ctypes.c_void_p()
         _check(lib.nerve_sampler_create(ctypes.byref(d), ctypes.byref(h)))
         self._h = h
