@@ -18,20 +18,14 @@ rocprofv3 counters when a summary of them is present under profiles/, and the
 CPU oracle timed on the host cores of the same machine on a bounded sample of
 the same workload.
 
-Profiling helpers (no JSON line):
-  --calibrate-copy MIB   after the timed steps, run 20 elementwise negations
-                         of MIB MiB each (a kernel that reads and writes a
-                         known number of bytes, to scale the byte counters)
-  --pmc-summary DIR      read the counter_collection.csv files that
-                         `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE`
-                         wrote under DIR and print the per-kernel averages and
-                         the calibrated traffic of the sampling kernel
+After the timed steps the last one is recomputed with the CPU oracle at the
+same tick (same logits, history, seeds, Philox stream) and the bench fails on
+any mismatch, so the path timed is the path checked. HBM traffic counters are
+collected separately (llmoop_amd/traffic.py).
 """
 from __future__ import annotations
 
 import argparse
-import csv
-import glob
 import json
 import os
 import re
@@ -46,7 +40,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 METRIC = "sampled rows/sec + µs/step at B=256×V=151936; % of HBM roofline"
 KERNEL = "sample_rows_kernel"
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "sample_rows_kernel_C5_traffic.txt")
+PROFILE_FILE = os.path.join(ROOT, "profiles", "sample_rows_kernel_{}_profile.md")
 
 
 def parse():
@@ -60,10 +54,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--cpu-threads", type=int, default=0, help="host threads of the CPU baseline (0: up to 16)")
     ap.add_argument("--slices", type=int, default=0, help="workgroups per row (0 = automatic)")
-    ap.add_argument("--variant", default="", help="diagnostics: no-history | greedy | no-penalty")
-    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB")
-    ap.add_argument("--pmc-summary", default="", metavar="DIR")
-    ap.add_argument("--no-tick-check", action="store_true", help="diagnostics: skip the stream-tick check")
+    ap.add_argument("--no-check", action="store_true", help="skip the oracle check of the last timed step")
     return ap.parse_args()
 
 
@@ -96,51 +87,11 @@ def cpu_baseline(w, budget_s: float, threads: int = 0) -> dict:
     }
 
 
-def read_counters(directory: str) -> dict:
-    """{kernel name: {counter: [per-dispatch values]}} from rocprofv3 CSVs."""
-    out: dict = {}
-    for path in glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True):
-        with open(path) as f:
-            for r in csv.DictReader(f):
-                per = out.setdefault(r["Kernel_Name"], {}).setdefault(r["Counter_Name"], {})
-                key = r.get("Dispatch_Id") or r.get("Correlation_Id") or str(len(per))
-                per[key] = per.get(key, 0.0) + float(r["Counter_Value"])
-    return {k: {c: list(v.values()) for c, v in d.items()} for k, d in out.items()}
-
-
-def pmc_summary(directory: str, copy_mib: int) -> None:
-    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the sampling kernel,
-    scaled by what the same counters read for the known-size negation kernel:
-    factor = known bytes / counted bytes."""
-    counters = read_counters(directory)
-    copy_bytes = copy_mib * 2**20
-    rows = []
-    for name, d in counters.items():
-        for c, v in d.items():
-            rows.append((name, c, float(np.mean(v)), len(v)))
-    for name, c, mean, n in sorted(rows):
-        print(f"{c:10s} {mean:14.1f} KiB  n={n:4d}  {name[:100]}")
-    def pick(pattern, counter):
-        vals = [m for name, c, m, _ in rows if c == counter and re.search(pattern, name)]
-        return max(vals) if vals else None
-    fetch, write = pick(KERNEL, "FETCH_SIZE"), pick(KERNEL, "WRITE_SIZE")
-    cfetch, cwrite = pick("neg_kernel", "FETCH_SIZE"), pick("neg_kernel", "WRITE_SIZE")
-    if fetch is None or cfetch is None:
-        print("missing sampling-kernel or copy-kernel counters")
-        return
-    fr = copy_bytes / (cfetch * 1024.0)
-    wr = copy_bytes / (cwrite * 1024.0) if cwrite else 1.0
-    traffic = fetch * 1024.0 * fr + (write or 0.0) * 1024.0 * wr
-    print(f"calibration kernel: {copy_bytes} B read and written; FETCH_SIZE {cfetch:.1f} KiB -> factor {fr:.4f}; "
-          f"WRITE_SIZE {cwrite} KiB -> factor {wr:.4f}")
-    print(f"traffic_bytes_per_launch = {traffic:.0f}")
-
-
 def measured_traffic(workload: str):
     """Calibrated HBM bytes per launch from the committed counter summary of
     this workload, or None."""
     try:
-        text = open(TRAFFIC_FILE).read()
+        text = open(PROFILE_FILE.format(workload)).read()
     except OSError:
         return None
     if f"workload: {workload}" not in text:
@@ -151,9 +102,6 @@ def measured_traffic(workload: str):
 
 def main():
     args = parse()
-    if args.pmc_summary:
-        pmc_summary(args.pmc_summary, args.calibrate_copy or 256)
-        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(rows are independent: B rows shard over GPUs with no exchange)", file=sys.stderr)
@@ -165,14 +113,6 @@ def main():
 
     dev = torch.device("cuda:0")
     w = workloads.make(args.config, seed=2024, step=0)
-    if args.variant == "no-history":
-        w.history = w.history_len = None
-    elif args.variant == "greedy":
-        w.params["method"] = 0
-    elif args.variant == "no-penalty":
-        w.params["repetition_penalty"] = 1.0
-        w.params["frequency_penalty"] = 0.0
-        w.params["presence_penalty"] = 0.0
     B, V = w.batch, w.vocab
     sampler = S.Sampler(V, B, dtype=w.dtype, top_k_capacity=w.top_k_capacity,
                         history_capacity=0 if w.history is None else w.history.shape[1],
@@ -218,19 +158,28 @@ def main():
     device_s = start.elapsed_time(end) / 1e3 / args.steps
 
     tick = stream_control[:, 1].cpu().numpy().view(np.uint32)
-    assert args.no_tick_check or (tick == args.warmup + args.steps).all(), "stream ticks did not advance once per step"
+    if not (tick == args.warmup + args.steps).all():
+        sys.exit("bench.py: stream ticks did not advance once per step")
+    parity = None
+    if not args.no_check:
+        # the last timed step (tick warmup + steps - 1) recomputed by the oracle
+        from oracle import oracle
 
-    if args.calibrate_copy:
-        n = args.calibrate_copy * 2**20 // 4
-        src = torch.ones(n, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(20):
-            torch.neg(src, out=dst)  # one elementwise kernel: reads and writes exactly MIB MiB
-        torch.cuda.synchronize()
+        last = args.warmup + args.steps - 1
+        ref = oracle.sample(w.logits, w.params, top_k_capacity=w.top_k_capacity, history=w.history,
+                            history_len=w.history_len, allowed=w.allowed, seeds=w.seeds,
+                            steps=np.full(B, last, np.uint64), rng=w.rng, eos_token_id=w.eos_token_id,
+                            threads=min(os.cpu_count() or 1, 16))
+        got = out.cpu().numpy().view(np.uint32)
+        bad = int((got != ref["out"]).any(axis=1).sum())
+        parity = {"rows_checked": B, "rows_mismatched": bad, "tick": last, "checker": "oracle (CPU)"}
+        if bad:
+            print(json.dumps({"parity": parity}), flush=True)
+            sys.exit(f"bench.py: {bad} of {B} rows of the last timed step differ from the oracle")
 
     alg_bytes = w.algorithmic_bytes()
     achieved = alg_bytes / device_s / 1e9
-    traffic = measured_traffic(w.name) if not args.variant and args.slices == 0 else None
+    traffic = measured_traffic(w.name) if args.slices == 0 else None
     res = {
         "metric": METRIC,
         "value": B * args.steps / wall,
@@ -267,6 +216,7 @@ def main():
             "device_us_per_step": device_s * 1e6,
             "algorithmic_bytes": alg_bytes,
         },
+        "parity": parity,
     }
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds, args.cpu_threads)
