@@ -241,11 +241,13 @@ int nerve_sampler_step(nerve_sampler *sampler, const nerve_sampler_batch *batch,
 /* nerve_sampler_step that allocates nothing. No counterpart in the reference: it is
  * for callers that cannot allocate device memory (HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc). Steps whose rows need several slices take
- * their cross-workgroup scratch (batch x slices x top_k_capacity x 8 bytes + 4 bytes per
- * (row, slice)) from one static array of 4 MiB per GPU instead of the handle's; larger
- * needs return NERVE_ERR_INVALID_ARGUMENT. Every call on a GPU shares that array, so
- * calls that overlap on one GPU (other streams, other handles) race; the array's
- * contents need no clearing between calls. Results equal nerve_sampler_step's. */
+ * their cross-workgroup scratch (64 KiB of per-row arrival counts, then batch x slices x
+ * top_k_capacity x 8 bytes + 4 bytes per (row, slice)) from one static array of 4 MiB per
+ * GPU instead of the handle's; larger needs return NERVE_ERR_INVALID_ARGUMENT. Every call
+ * on a GPU shares that array, so calls that overlap on one GPU (other streams, other
+ * handles) race. The counts start at zero when the library loads and every step leaves
+ * them at zero; nothing else needs clearing between calls. Results equal
+ * nerve_sampler_step's. */
 int nerve_sampler_step_static_scratch(nerve_sampler *sampler, const nerve_sampler_batch *batch, void *stream);
 
 /* Sets bits for token ids < vocab_size into per-row seen bitmaps:

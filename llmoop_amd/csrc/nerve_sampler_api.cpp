@@ -43,6 +43,18 @@ uint32_t next_pow2(uint32_t v) {
     return p;
 }
 
+// Automatic slices per row: rows of 256 KiB or more in batches below 128
+// rows split three ways at most (enough workgroups to use more CUs, each
+// slice merged by the row's last one), measured on MI355X: B=64 x V=151936
+// bf16 15.7 us with 3 slices against 17.2 with 1; B=32 x V=32000 and B=1
+// stay fastest with one.
+uint32_t auto_slices(const nerve_sampler_desc &d, uint32_t batch) {
+    const uint64_t row_bytes = (uint64_t)d.vocab_size * (d.dtype == NERVE_DTYPE_F32 ? 4u : 2u);
+    if (row_bytes < (256u << 10) || batch >= 128u || batch == 0u) return 1u;
+    const uint32_t s = (192u + batch - 1u) / batch;
+    return s < 3u ? s : 3u;
+}
+
 uint32_t log2u(uint32_t v) {
     uint32_t l = 0;
     while ((1u << l) < v) ++l;
@@ -59,6 +71,7 @@ struct nerve_sampler {
     uint32_t last_slices;      // workgroups per row of the last step
     uint2 *scratch_lists;
     uint32_t *scratch_meta;
+    uint32_t *scratch_counts;  // [max_batch] arrival counts of the in-kernel merge, zero between steps
     size_t lds_per_block;      // hipDeviceProp_t::sharedMemPerBlock
 };
 
@@ -196,19 +209,27 @@ int nerve_sampler_create(const nerve_sampler_desc *desc, nerve_sampler **out) {
 
     // Workgroups per row: a workgroup holds its slice of the row in VGPRs, so
     // a slice is at most block_threads() * max_vectors_per_lane() lane-vectors
-    // (raised per step to what the row needs). Automatic: one slice where the
-    // row fits, since a second slice costs the merge launch, which measured
-    // more than the bandwidth it adds at small batches (C1 8.6 vs 10.5 µs, C2
-    // 11.0 vs 14.1 µs on MI355X).
+    // (raised per step to what the row needs). Automatic (slices_per_row 0):
+    // auto_slices() per step.
     const uint32_t threads = nerve::block_threads();
     uint32_t want = d.slices_per_row;
     if (want == 0u) want = 1u;
-    // The one-element-per-load kernels hold the fewest tokens per slice.
-    const uint32_t scalar_tokens = threads * nerve::max_vectors_per_lane(nerve::kVariantF32Scalar);
-    const uint32_t need = (d.vocab_size + scalar_tokens - 1u) / scalar_tokens;
-    const uint32_t capacity = want > need ? want : need;
+    // Slices the scratch holds: what 16-byte aligned rows of this dtype need
+    // (or more when asked), the automatic split of large rows, and the more
+    // slices of the one-element-per-load kernels for unaligned rows when the
+    // merge area allows them (otherwise such steps are rejected).
+    const uint32_t vvar = d.dtype == NERVE_DTYPE_F32 ? nerve::kVariantF32Vec : nerve::kVariantBf16Vec;
+    const uint32_t vec_tokens = threads * nerve::max_vectors_per_lane(vvar) * nerve::elems_per_vector(vvar);
+    const uint32_t vec_need = (d.vocab_size + vec_tokens - 1u) / vec_tokens;
+    uint32_t capacity = want > vec_need ? want : vec_need;
+    if (d.slices_per_row == 0u && auto_slices(d, 1u) > capacity) capacity = auto_slices(d, 1u);
     if ((uint64_t)capacity * d.top_k_capacity > 12288u)
         return fail(NERVE_ERR_INVALID_SAMPLING_SPEC, "slices_per_row * top_k_capacity exceeds the 12288-entry merge area");
+    if (capacity > 64u) return fail(NERVE_ERR_INVALID_ARGUMENT, "slices_per_row must be at most 64");
+    const uint32_t scalar_tokens = threads * nerve::max_vectors_per_lane(nerve::kVariantF32Scalar);
+    const uint32_t scalar_need = (d.vocab_size + scalar_tokens - 1u) / scalar_tokens;
+    if (scalar_need > capacity && (uint64_t)scalar_need * d.top_k_capacity <= 12288u && scalar_need <= 64u)
+        capacity = scalar_need;
 
     nerve_sampler *s = new (std::nothrow) nerve_sampler();
     if (!s) return fail(NERVE_ERR_INVALID_ARGUMENT, "out of host memory");
@@ -222,7 +243,8 @@ int nerve_sampler_create(const nerve_sampler_desc *desc, nerve_sampler **out) {
         const uint32_t per = threads * nerve::max_vectors_per_lane(v);
         const uint32_t nvec = d.vocab_size / nerve::elems_per_vector(v);
         const uint32_t need_v = nvec ? (nvec + per - 1u) / per : 1u;
-        s->last_slices = want > need_v ? want : need_v;
+        const uint32_t w = d.slices_per_row ? want : auto_slices(d, d.max_batch);
+        s->last_slices = w > need_v ? w : need_v;
     }
     s->lds_per_block = prop.sharedMemPerBlock;
     int prev = 0;
@@ -233,6 +255,8 @@ int nerve_sampler_create(const nerve_sampler_desc *desc, nerve_sampler **out) {
     if (!(d.flags & NERVE_DESC_NO_SCRATCH)) {
         e = hipMalloc((void **)&s->scratch_lists, lists_bytes);
         if (e == hipSuccess) e = hipMalloc((void **)&s->scratch_meta, meta_bytes);
+        if (e == hipSuccess) e = hipMalloc((void **)&s->scratch_counts, (size_t)d.max_batch * sizeof(uint32_t));
+        if (e == hipSuccess) e = hipMemset(s->scratch_counts, 0, (size_t)d.max_batch * sizeof(uint32_t));
         if (e == hipSuccess) e = hipDeviceSynchronize();
     }
     (void)hipSetDevice(prev);
@@ -252,6 +276,7 @@ int nerve_sampler_destroy(nerve_sampler *s) {
     (void)hipSetDevice(s->device);
     if (s->scratch_lists) (void)hipFree(s->scratch_lists);
     if (s->scratch_meta) (void)hipFree(s->scratch_meta);
+    if (s->scratch_counts) (void)hipFree(s->scratch_counts);
     (void)hipSetDevice(prev);
     delete s;
     return NERVE_OK;
@@ -310,10 +335,17 @@ int step_impl(nerve_sampler *s, const nerve_sampler_batch *b, void *stream, bool
     const uint32_t epv = nerve::elems_per_vector(variant);
     const uint32_t nvec = d.vocab_size / epv;  // full slots; the V % epv tail goes to the last slice
     const uint32_t per_slice_max = nerve::block_threads() * nerve::max_vectors_per_lane(variant);
-    uint32_t slices = s->slices;
+    uint32_t slices = d.slices_per_row ? s->slices : auto_slices(d, b->batch);
     const uint32_t slices_need = (nvec + per_slice_max - 1u) / per_slice_max;
     if (slices < slices_need) slices = slices_need;
-    if (slices > s->slices_capacity) return fail(NERVE_ERR_INVALID_ARGUMENT, "vocabulary needs more slices than the scratch holds");
+    if (slices > s->slices_capacity) {
+        char buf[200];
+        std::snprintf(buf, sizeof(buf),
+                      "rows of this vocabulary need %u slices with %s logits rows; the handle holds %u (pass "
+                      "16-byte aligned rows and strides)",
+                      slices, vec_ok ? "aligned" : "unaligned", s->slices_capacity);
+        return fail(NERVE_ERR_INVALID_ARGUMENT, buf);
+    }
     const uint32_t vec_per_slice = (nvec + slices - 1u) / slices;
     const uint32_t nv = nerve::vectors_per_lane(variant, (vec_per_slice + nerve::block_threads() - 1u) / nerve::block_threads());
     if (nv == 0u) return fail(NERVE_ERR_INVALID_ARGUMENT, "slice exceeds the kernel's register capacity");
@@ -341,6 +373,8 @@ int step_impl(nerve_sampler *s, const nerve_sampler_batch *b, void *stream, bool
     a.topk_probs = b->topk_probs;
     a.scratch_lists = s->scratch_lists;
     a.scratch_meta = s->scratch_meta;
+    a.scratch_counts = s->scratch_counts;
+    a.merge_in_kernel = slices * d.top_k_capacity <= nerve::kernel_merge_capacity() ? 1u : 0u;
     a.vocab = d.vocab_size;
     a.batch = b->batch;
     a.slices = slices;
@@ -392,20 +426,22 @@ int step_impl(nerve_sampler *s, const nerve_sampler_batch *b, void *stream, bool
     if (slices > 1u) {
         const size_t lists = (size_t)b->batch * slices * d.top_k_capacity * sizeof(uint2);
         const size_t meta = (size_t)b->batch * slices * sizeof(uint32_t);
+        const size_t counts = (size_t)nerve::kStaticMaxRows * sizeof(uint32_t);
         if (static_scratch) {
-            if (lists + meta > nerve::kStaticScratchBytes) {
+            if (counts + lists + meta > nerve::kStaticScratchBytes || b->batch > nerve::kStaticMaxRows) {
                 char buf[200];
                 std::snprintf(buf, sizeof(buf),
                               "step needs %zu bytes of scratch (batch x slices x top_k_capacity), the static array "
                               "holds %zu",
-                              lists + meta, nerve::kStaticScratchBytes);
+                              counts + lists + meta, nerve::kStaticScratchBytes);
                 return fail(NERVE_ERR_INVALID_ARGUMENT, buf);
             }
             void *base = nullptr;
             const hipError_t e = nerve::static_scratch(s->device, &base);
             if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
-            a.scratch_lists = (uint2 *)base;
-            a.scratch_meta = (uint32_t *)((uint8_t *)base + lists);
+            a.scratch_counts = (uint32_t *)base;
+            a.scratch_lists = (uint2 *)((uint8_t *)base + counts);
+            a.scratch_meta = (uint32_t *)((uint8_t *)base + counts + lists);
         } else if (!s->scratch_lists) {
             return fail(NERVE_ERR_INVALID_ARGUMENT,
                         "this handle was created with NERVE_DESC_NO_SCRATCH: steps with several slices per row go "

@@ -1126,7 +1126,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     lds_sync();
     // the uniform draw depends only on the seed and tick: one wave computes it
     // now, off the finish's critical path
-    if (sampled && a.slices == 1u && wave == 1u) {
+    if (sampled && wave == 1u) {
         const float uu = random_unit(a.rng, io.seed, (uint64_t)io.tick_lo | ((uint64_t)io.tick_hi << 32), row);
         if (lane == 0u) sm.u = uu;
     }
@@ -1726,12 +1726,50 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     lds_sync();
 
 
-    // 8. publish: with several slices the sorted list goes to scratch and the
-    // finish kernel merges the row; a single slice finishes here.
+    // 8. publish: with several slices the sorted list goes to scratch; the
+    // last slice of the row to arrive merges the row's lists and finishes it
+    // (or, when the lists exceed its merge area, the finish kernel does). A
+    // single slice finishes here.
     if (a.slices > 1) {
         uint2 *lists = a.scratch_lists + (uint64_t)(row * a.slices + slice) * a.kcap;
-        for (uint32_t i = tid; i < n_out; i += kBlock) lists[i] = s_sorted[i];
-        if (tid == 0) a.scratch_meta[row * a.slices + slice] = n_out | (flags_slice << 16);
+        uint32_t *meta = a.scratch_meta + row * a.slices;
+        if (!a.merge_in_kernel) {
+            for (uint32_t i = tid; i < n_out; i += kBlock) lists[i] = s_sorted[i];
+            if (tid == 0) meta[slice] = n_out | (flags_slice << 16);
+            return;
+        }
+        // Written through to memory (system-scope stores) and completed before
+        // the arrival count, so the last slice, on whichever XCD it runs,
+        // reads them with loads that bypass the caches.
+        for (uint32_t i = tid; i < n_out; i += kBlock) {
+            const uint2 e = s_sorted[i];
+            __hip_atomic_store((uint64_t *)&lists[i], ((uint64_t)e.y << 32) | e.x, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+        if (tid == 0)
+            __hip_atomic_store(&meta[slice], n_out | (flags_slice << 16), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this lane's stores are complete
+        __syncthreads();
+        if (tid == 0) sm.flag[0] = __hip_atomic_fetch_add(&a.scratch_counts[row], 1u, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_SYSTEM);
+        __syncthreads();
+        if (sm.flag[0] != a.slices - 1u) return;
+        // the last slice: the count is reset for the next step (every slice
+        // of this one has arrived), then the merge and the finish
+        if (tid == 0) __hip_atomic_store(&a.scratch_counts[row], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        const uint2 *all = a.scratch_lists + (uint64_t)row * a.slices * a.kcap;
+        uint32_t row_flags;
+        const uint32_t n = merge_slices<kBlock>(
+            a, k, s_big, s_sorted, sm.hist, row_flags,
+            [&](uint32_t i) {
+                const uint64_t v = __hip_atomic_load((const uint64_t *)&all[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+            },
+            [&](uint32_t s) { return __hip_atomic_load(&meta[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM); });
+        const RowIo io_m = {sm.io[0], sm.io[1], sm.io[2], sm.io[3]};
+        const RowCtx ctx_row = row_ctx<Elem, PEN>(a, row, P, s_hash);
+        finish_row<Elem, PEN, kBlock>(a, row, io_m, P, k, sampled, n, row_flags, s_sorted, s_big, (float *)s_sslot,
+                                      (float *)s_big + 64, s_hash, ctx_row, sm.u);
         return;
     }
     const RowIo io_l = {sm.io[0], sm.io[1], sm.io[2], sm.io[3]};
@@ -1739,49 +1777,39 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
                                   (float *)s_big + 64, s_hash, ctx, sm.u);
 }
 
-// Merges the S sorted slice lists of each row (one workgroup per row) and
-// finishes the row. Launched after sample_rows_kernel on the same stream, so
-// the slice lists are visible without any cross-workgroup fence.
-template <typename Elem, int PEN>
-__global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
-    extern __shared__ uint32_t s_dyn[];
-    uint32_t *s_hash = s_dyn;
-    uint2 *s_big = (uint2 *)(s_dyn + a.hash_slots);
-    uint2 *s_sorted = s_big + a.big_entries;
-    float *s_wt = (float *)(s_sorted + a.kcap);  // [kcap] weights
+// Merges the S sorted slice lists of a row into s_sorted[0 .. n) (n = min(k,
+// total)): the lists go to s_big through load_entry(i) (entry i of the row's
+// S * kcap), the counts and flags to s_meta through load_meta(s); an entry's
+// rank is its position in its own list plus the number of better entries in
+// every other list (binary search; ids are distinct). row_flags gets the OR
+// of the slices' flags. Ends with a block barrier.
+template <int NT, typename LoadEntry, typename LoadMeta>
+__device__ __forceinline__ uint32_t merge_slices(const StepArgs &a, uint32_t k, uint2 *s_big, uint2 *s_sorted,
+                                                 uint32_t *s_meta, uint32_t &row_flags, LoadEntry load_entry,
+                                                 LoadMeta load_meta) {
     const uint32_t tid = threadIdx.x;
-    const uint32_t row = blockIdx.x;
-    const nerve_sampler_row_params P = a.params[row];
-    const RowIo io = load_row_io(a, row);
-    const bool sampled = P.method != NERVE_METHOD_GREEDY;
-    uint32_t k = sampled ? P.top_k : 1u;
-    k = k < 1u ? 1u : (k > a.kcap ? a.kcap : k);
-    const float u = sampled ? random_unit(a.rng, io.seed, (uint64_t)io.tick_lo | ((uint64_t)io.tick_hi << 32), row) : 0.0f;
-
     // every list entry is copied, whatever the counts (entries past a count
     // are ignored below), so the list loads do not wait for the counts
-    const uint2 *all = a.scratch_lists + (uint64_t)row * a.slices * a.kcap;
-    const uint32_t *meta = a.scratch_meta + row * a.slices;
     const uint32_t ne = a.slices * a.kcap;
-    for (uint32_t i = tid; i < ne; i += kFinishBlock) s_big[i] = all[i];
-    uint32_t total = 0, row_flags = 0;
+    for (uint32_t i = tid; i < ne; i += NT) s_big[i] = load_entry(i);
+    if (tid < a.slices) s_meta[tid] = load_meta(tid);
+    __syncthreads();
+    uint32_t total = 0;
+    row_flags = 0;
     for (uint32_t s = 0; s < a.slices; ++s) {
-        const uint32_t m = meta[s];
+        const uint32_t m = s_meta[s];
         total += m & 0xffffu;
         row_flags |= m >> 16;
     }
-    __syncthreads();
-    // rank of an entry = its position in its own sorted list plus the number
-    // of better entries in every other list (binary search); ids are distinct
-    for (uint32_t i = tid; i < ne; i += kFinishBlock) {
+    for (uint32_t i = tid; i < ne; i += NT) {
         const uint32_t s = i / a.kcap, pos = i % a.kcap;
-        if (pos >= (meta[s] & 0xffffu)) continue;
+        if (pos >= (s_meta[s] & 0xffffu)) continue;
         const uint2 e = s_big[i];
         uint32_t r = pos;
         for (uint32_t o = 0; o < a.slices && r < k; ++o) {
             if (o == s) continue;
             const uint2 *lo = s_big + o * a.kcap;
-            uint32_t lo_i = 0, hi_i = meta[o] & 0xffffu;
+            uint32_t lo_i = 0, hi_i = s_meta[o] & 0xffffu;
             while (lo_i < hi_i) {
                 const uint32_t mid = (lo_i + hi_i) >> 1;
                 if (entry_better(lo[mid], e)) lo_i = mid + 1; else hi_i = mid;
@@ -1790,9 +1818,15 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
         }
         if (r < k) s_sorted[r] = e;
     }
-    const uint32_t n = total < k ? total : k;
     __syncthreads();
+    return total < k ? total : k;
+}
 
+// The row's context for recomputing configured values over the whole row
+// (no slice-local LDS bitmap).
+template <typename Elem, int PEN>
+__device__ __forceinline__ RowCtx row_ctx(const StepArgs &a, uint32_t row, const nerve_sampler_row_params &P,
+                                          uint32_t *s_hash) {
     RowCtx ctx;
     ctx.logits_row = (const Elem *)a.logits + (uint64_t)row * a.ld;
     ctx.allowed_row = a.allowed ? a.allowed + (uint64_t)row * a.allowed_stride : nullptr;
@@ -1807,6 +1841,34 @@ __global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
     ctx.history = PEN == 2;
     ctx.prefix = PEN == 1 && a.prefix_ids ? a.prefix_ids + (uint64_t)row * a.prefix_stride : nullptr;
     ctx.prefix_n = PEN == 1 ? prefix_count(a, row) : 0u;
+    return ctx;
+}
+
+// Merges the S sorted slice lists of each row (one workgroup per row) and
+// finishes the row, when the slice kernel does not (slices * kcap larger
+// than its merge area). Launched after sample_rows_kernel on the same
+// stream, so the slice lists are visible without any cross-workgroup fence.
+template <typename Elem, int PEN>
+__global__ __launch_bounds__(kFinishBlock) void finish_rows_kernel(StepArgs a) {
+    extern __shared__ uint32_t s_dyn[];
+    __shared__ uint32_t s_meta[64];
+    uint32_t *s_hash = s_dyn;
+    uint2 *s_big = (uint2 *)(s_dyn + a.hash_slots);
+    uint2 *s_sorted = s_big + a.big_entries;
+    float *s_wt = (float *)(s_sorted + a.kcap);  // [kcap] weights
+    const uint32_t row = blockIdx.x;
+    const nerve_sampler_row_params P = a.params[row];
+    const RowIo io = load_row_io(a, row);
+    const bool sampled = P.method != NERVE_METHOD_GREEDY;
+    uint32_t k = sampled ? P.top_k : 1u;
+    k = k < 1u ? 1u : (k > a.kcap ? a.kcap : k);
+    const float u = sampled ? random_unit(a.rng, io.seed, (uint64_t)io.tick_lo | ((uint64_t)io.tick_hi << 32), row) : 0.0f;
+    const uint2 *all = a.scratch_lists + (uint64_t)row * a.slices * a.kcap;
+    const uint32_t *meta = a.scratch_meta + row * a.slices;
+    uint32_t row_flags;
+    const uint32_t n = merge_slices<kFinishBlock>(a, k, s_big, s_sorted, s_meta, row_flags,
+                                                  [&](uint32_t i) { return all[i]; }, [&](uint32_t s) { return meta[s]; });
+    const RowCtx ctx = row_ctx<Elem, PEN>(a, row, P, s_hash);
     finish_row<Elem, PEN, kFinishBlock>(a, row, io, P, k, sampled, n, row_flags, s_sorted, s_big, s_wt, (float *)s_big,
                                         s_hash, ctx, u);
 }
@@ -1838,7 +1900,7 @@ static hipError_t launch_one(const StepArgs &a, hipStream_t stream) {
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(kern, dim3(a.batch * a.slices), dim3(kBlock), a.dyn_lds_bytes, stream, a);
     e = hipGetLastError();
-    if (e != hipSuccess || a.slices == 1u) return e;
+    if (e != hipSuccess || a.slices == 1u || a.merge_in_kernel) return e;
     auto fin = finish_rows_kernel<Elem, PEN>;
     e = ensure_dyn_lds(fin, a.device, a.finish_lds_bytes, fin_set);
     if (e != hipSuccess) return e;

@@ -37,6 +37,8 @@ struct StepArgs {
     float *topk_probs;
     uint2 *scratch_lists;    // [max_batch][slices][kcap] sorted slice survivors
     uint32_t *scratch_meta;  // [max_batch][slices]: count | flags << 16
+    uint32_t *scratch_counts;  // [max_batch] slices of the row that have arrived (zero between steps)
+    uint32_t merge_in_kernel;  // the last slice of a row merges and finishes it
     uint32_t vocab;
     uint32_t batch;
     uint32_t slices;
@@ -68,6 +70,9 @@ struct StepArgs {
 // (per GPU): slice lists of batch x slices x top_k_capacity entries of 8 bytes
 // plus 4 bytes of metadata per (row, slice).
 constexpr size_t kStaticScratchBytes = (size_t)4 << 20;
+// The static array starts with the per-row arrival counts (zero at load,
+// reset by each step), then the lists and metadata.
+constexpr uint32_t kStaticMaxRows = 16384;
 constexpr int kMaxDevices = 64;
 // Device address of this GPU's static scratch array (the current device must
 // be `device`); taken once per device.
@@ -76,6 +81,7 @@ hipError_t static_scratch(int device, void **ptr);
 uint32_t elems_per_vector(uint32_t variant);
 uint32_t block_threads();
 uint32_t merge_capacity();
+uint32_t kernel_merge_capacity();  // slice-list entries the slice kernel itself can merge
 uint32_t stream_lds_bytes(uint32_t variant, bool mask, bool pen, uint32_t hash_slots, uint32_t bitmap_words,
                           uint32_t kcap);
 uint32_t max_vectors_per_lane(uint32_t variant);

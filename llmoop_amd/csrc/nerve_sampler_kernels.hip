@@ -82,6 +82,7 @@ uint32_t elems_per_vector(uint32_t variant) {
 
 uint32_t block_threads() { return (uint32_t)kBlock; }
 uint32_t merge_capacity() { return kCandCap; }
+uint32_t kernel_merge_capacity() { return kStreamCandCap; }
 
 // LDS of the slice kernel, in its layout order: staged lane-vectors and their
 // slots, candidates, the sorted list, the history table, the penalty bitmap
