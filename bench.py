@@ -48,7 +48,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", default="C5", help="C1..C5 (C5 is the headline workload)")
+    ap.add_argument("--config", default="C5", help="C1..C5, C5P (C5 is the headline workload)")
     ap.add_argument("--buffers", type=int, default=4, help="logits copies the steps rotate over")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
@@ -199,7 +199,7 @@ def main():
             "batch": B,
             "vocab": V,
             "logits_dtype": w.dtype,
-            "top_k": 50 if w.name in ("C3", "C4", "C5") else int(w.params["top_k"][0]),
+            "top_k": 50 if w.name in ("C3", "C4", "C5", "C5P") else int(w.params["top_k"][0]),
             "history": 0 if w.history is None else int(w.history.shape[1]),
             "slices_per_row": sampler.slices_per_row,
             "logits_buffers": nbuf,

@@ -1336,12 +1336,14 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     }
     lds_sync();
     uint32_t nstaged = sm.flag[2];
+    uint32_t thr_stage = thr;  // the threshold the staged set was chosen with
     if (nstaged > kStageCap) {
         // The first half's threshold let too much through (a skewed row):
         // take the threshold of every report and stage again, reloading the
         // slice in chunks of 8 lane-vectors (the registers were released as
         // the stream went).
         set_thr(report_threshold(1));
+        thr_stage = thr;
         if (tid == 0) sm.flag[2] = 0u;
         lds_sync();
         constexpr int CH = 8;
@@ -1507,6 +1509,55 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     lds_sync();
     const uint32_t flags_slice = sm.flag[3];
     bool repad = false;  // the candidate list was rewritten: its padding is stale
+    if constexpr (PEN != 0) {
+        if (lowering && nstaged <= kStageCap && sm.flag[1] < k && thr_stage > kZeroKey) {
+            // Second chance, from registers: penalties pushed more than C - k
+            // of the raw reports below thr (typically a row whose top tokens
+            // are in its own history). Lane reports over the clean
+            // lane-vectors only (fully allowed, nothing penalised: there the
+            // configured key is the raw key) give a threshold t that at
+            // least k configured keys reach. The lane-vectors whose raw
+            // maximum lies in [t, thr_stage) join the staged set (their slots
+            // appended, the vectors gathered from memory by the whole
+            // workgroup, one load each), and the exact pass runs again over
+            // the whole set at t.
+            acc0 = VT::kAccInit;
+            acc1 = VT::kAccInit;
+            static_for<0, NV>([&](auto J) __attribute__((always_inline)) {
+                constexpr int j = J;
+                const uint32_t pw = (s_pen[(tok_base >> 5) + (uint32_t)j * kWordsPerJ] >> wsh) & kFull;
+                const bool clean = ((okm[j >> 5] >> (j & 31)) & 1u) && pw == 0u;
+                const uint32_t vm = clean ? vmx[j] : VT::kAccInit;
+                if (j & 1) acc1 = VT::merge(acc1, vm);
+                else acc0 = VT::merge(acc0, vm);
+            });
+            const uint32_t t = report_threshold(1);
+            if (t > kZeroKey) {
+                static_for<0, NV>([&](auto J) __attribute__((always_inline)) {
+                    constexpr int j = J;
+                    const bool lv = !MASK ? (uint32_t)j < nval : ((live[j >> 5] >> (j & 31)) & 1u) != 0u;
+                    if (lv && VT::ge_pos(vmx[j], t) && !VT::ge_pos(vmx[j], thr_stage)) {
+                        const uint32_t pos = atomicAdd(&sm.flag[2], 1u);
+                        if (pos < kStageCap) s_sslot[pos] = v0 + wbase + (uint32_t)j * 64u;
+                    }
+                });
+                lds_sync();
+                const uint32_t n2 = sm.flag[2];
+                const uint32_t n1 = nstaged;
+                nstaged = n2;  // past kStageCap: the exact selection from memory below
+                if (n2 <= kStageCap) {
+                    const vec_t *lvec = (const vec_t *)lrow;
+                    for (uint32_t i = n1 + tid; i < n2; i += kBlock) s_svec[i] = lvec[s_sslot[i]];
+                    if (tid == 0) sm.flag[1] = 0u;
+                    set_thr(t);
+                    lds_sync();
+                    push_staged();  // over all n2 staged lane-vectors
+                    lds_sync();
+                    repad = true;
+                }
+            }
+        }
+    }
     if (nstaged <= kStageCap && sm.flag[1] > kStreamCandCap && (PEN == 0 || lowering)) {
         repad = true;
         // Too many candidates for a weak threshold: the exact k-th key of the

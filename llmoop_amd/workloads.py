@@ -9,6 +9,8 @@ C1..C5 follow the configuration list that the benchmark is quoted on:
      offsets plus 200 scattered ids); B=128, V=128256, f32 ~ N(0, 2.5); some rows all-zero -> EOS 2
   C5 B=256, V=151936, bf16 ~ Student-t(df=4) * 2.0, 2048-id history, full penalty chain,
      top-k 50, top-p 0.9, T ~ U[0.5, 1.2] per row, Philox, consecutive steps
+  C5P C5 with each row's 2048 history ids drawn from that row's own 200 largest raw logits:
+     the penalties push the row's top tokens below the others (a decode row repeating itself)
 Logits are returned as float32 or as uint16 arrays holding bf16 bits
 (round-to-nearest-even from float32).
 """
@@ -129,15 +131,19 @@ def make(name: str, seed: int = 1234, step: int = 0, batch: int | None = None) -
         else:
             w.description = "full chain, B=64, V=151936, bf16, H=512"
         return w
-    if name == "C5":
+    if name in ("C5", "C5P"):
         B, V = batch or 256, 151936
         x = (rng.standard_t(4, size=(B, V)) * 2.0).astype(np.float32)
         H = 2048
         hist = rng.integers(0, V, (B, H)).astype(np.uint32)
+        if name == "C5P":
+            top = np.argpartition(-x, 200, axis=1)[:, :200]
+            hist = np.take_along_axis(top, rng.integers(0, 200, (B, H)), axis=1).astype(np.uint32)
         p = _params(B, temperature=rng.uniform(0.5, 1.2, B).astype(np.float32), top_k=50, top_p=0.9,
                     repetition_penalty=1.1, frequency_penalty=0.5, presence_penalty=0.3)
-        return Workload("C5", V, B, "bf16", to_bf16_bits(x), p, 64, RNG_PHILOX,
+        return Workload(name, V, B, "bf16", to_bf16_bits(x), p, 64, RNG_PHILOX,
                         rng.integers(0, 2**32, B, dtype=np.uint64).astype(np.uint32), np.full(B, step, np.uint64),
                         history=hist, history_len=np.full(B, H, np.uint32),
-                        description="large-batch decode: B=256, V=151936, bf16 Student-t, H=2048, per-row T")
+                        description="large-batch decode: B=256, V=151936, bf16 Student-t, H=2048, per-row T"
+                        + (", history from each row's own top 200" if name == "C5P" else ""))
     raise ValueError(f"unknown workload {name}")

@@ -156,7 +156,7 @@ def test_greedy_small_vocab_all_neg_inf_pads_with_vocab_id(oracle):
     assert list(gpu["token_id"]) == [10, 4]
 
 
-@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5"])
+@pytest.mark.parametrize("name", ["C1", "C2", "C3", "C4", "C5", "C5P"])
 def test_benchmark_configs_full_size(oracle, name):
     from llmoop_amd import workloads
 
@@ -205,6 +205,61 @@ def test_penalised_top_tokens_take_the_exact_path(oracle, dtype):
     # no survivor is one of the penalised top tokens
     for r in range(B):
         assert not set(gpu["topk_ids"][r][:50]) & set(hist[r, :150].tolist())
+
+
+PENALISED_TOP_CASES = [
+    # (label, dtype, V, row stride, slices, penalty state, mask, greedy rows)
+    ("mask-greedy-bf16", "bf16", 60000, 60000, 0, "history", True, True),
+    ("seen-f32", "f32", 50000, 50000, 0, "seen", False, False),
+    ("seen-mask-bf16", "bf16", 151936, 151936, 0, "seen", True, True),
+    ("unaligned-f32", "f32", 30001, 30003, 0, "history", False, True),
+    ("slices3-bf16", "bf16", 100000, 100000, 3, "history", True, False),
+    ("counts-f32", "f32", 128256, 128256, 0, "history", False, False),
+]
+
+
+@pytest.mark.parametrize("label,dtype,V,stride,slices,pen,mask,greedy", PENALISED_TOP_CASES,
+                         ids=[c[0] for c in PENALISED_TOP_CASES])
+def test_penalised_top_tokens_variants(oracle, label, dtype, V, stride, slices, pen, mask, greedy):
+    """Rows whose largest raw logits are all penalised (history drawn from the
+    row's own top tokens), across the kernel variants: masked rows with
+    greedy rows among them, seen bitmaps, unaligned rows (one element per
+    load), several slices per row, and repeat counts that drive the
+    frequency penalty."""
+    from llmoop_amd.workloads import to_bf16_bits
+
+    rng = np.random.default_rng(zlib.crc32(label.encode()) & 0xFFFF)
+    B, H = 8, 512
+    x = (rng.standard_t(4, size=(B, stride)) * 2.0).astype(np.float32)
+    top = np.argsort(-x[:, :V], axis=1)[:, :160]
+    params = _random_params(rng, B, 64, method=1)
+    params["top_k"] = rng.integers(20, 65, B)
+    params["repetition_penalty"] = rng.uniform(1.05, 3.0, B)
+    params["frequency_penalty"] = rng.uniform(0.0, 0.8, B)
+    params["presence_penalty"] = rng.uniform(0.0, 0.8, B)
+    if greedy:
+        params["method"][::3] = 0
+    kw = dict(seeds=rng.integers(0, 2**32, B, dtype=np.uint64).astype(np.uint32),
+              steps=rng.integers(0, 2**40, B, dtype=np.uint64))
+    W = (V + 31) // 32
+    if pen == "history":
+        kw["history"] = np.take_along_axis(top, rng.integers(0, top.shape[1], (B, H)), axis=1).astype(np.uint32)
+        kw["history_len"] = np.full(B, H, np.uint32)
+    else:
+        bits = np.zeros((B, W * 32), bool)
+        np.put_along_axis(bits, top, True, axis=1)
+        weights = np.uint64(1) << np.arange(32, dtype=np.uint64)
+        kw["seen"] = (bits.reshape(B, W, 32).astype(np.uint64) * weights).sum(axis=2).astype(np.uint32)
+    if mask:
+        allow = rng.random((B, W * 32)) < 0.7
+        allow[:, V:] = False
+        weights = np.uint64(1) << np.arange(32, dtype=np.uint64)
+        kw["allowed"] = (allow.reshape(B, W, 32).astype(np.uint64) * weights).sum(axis=2).astype(np.uint32)
+    logits = to_bf16_bits(x) if dtype == "bf16" else x
+    _say(f"penalised top {label}")
+    ref = oracle.sample(logits, params, top_k_capacity=64, vocab_size=V, threads=8, **kw)
+    gpu = run_gpu(logits, params, top_k_capacity=64, vocab=V, slices_per_row=slices, **kw)
+    assert_parity(gpu, ref, params, label=label, prob_rtol=1e-5 if dtype == "f32" else 2e-3)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
