@@ -1533,14 +1533,34 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
             });
             const uint32_t t = report_threshold(1);
             if (t > kZeroKey) {
+                // lane-vectors to append, counted per lane, then one LDS
+                // atomic per wave
+                uint32_t am[LW];
+#pragma unroll
+                for (int i = 0; i < LW; ++i) am[i] = 0u;
                 static_for<0, NV>([&](auto J) __attribute__((always_inline)) {
                     constexpr int j = J;
-                    const bool lv = !MASK ? (uint32_t)j < nval : ((live[j >> 5] >> (j & 31)) & 1u) != 0u;
-                    if (lv && VT::ge_pos(vmx[j], t) && !VT::ge_pos(vmx[j], thr_stage)) {
-                        const uint32_t pos = atomicAdd(&sm.flag[2], 1u);
-                        if (pos < kStageCap) s_sslot[pos] = v0 + wbase + (uint32_t)j * 64u;
-                    }
+                    const bool lv = ((live[j >> 5] >> (j & 31)) & 1u) != 0u;
+                    if (lv && VT::ge_pos(vmx[j], t) && !VT::ge_pos(vmx[j], thr_stage)) am[j >> 5] |= 1u << (j & 31);
                 });
+                uint32_t cnt = 0u;
+#pragma unroll
+                for (int i = 0; i < LW; ++i) cnt += (uint32_t)__builtin_popcount(am[i]);
+                const uint32_t incl = wave_inclusive_scan(cnt);
+                const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+                uint32_t pos0 = 0u;
+                if (lane == 63u && total) pos0 = atomicAdd(&sm.flag[2], total);
+                uint32_t pos = (uint32_t)__builtin_amdgcn_readlane((int)pos0, 63) + incl - cnt;
+#pragma unroll
+                for (int i = 0; i < LW; ++i) {
+                    uint32_t m = am[i];
+                    while (m) {
+                        const uint32_t j = (uint32_t)i * 32u + (uint32_t)__builtin_ctz(m);
+                        m &= m - 1u;
+                        if (pos < kStageCap) s_sslot[pos] = v0 + wbase + j * 64u;
+                        ++pos;
+                    }
+                }
                 lds_sync();
                 const uint32_t n2 = sm.flag[2];
                 const uint32_t n1 = nstaged;
