@@ -250,6 +250,40 @@ int nerve_sampler_step(nerve_sampler *sampler, const nerve_sampler_batch *batch,
  * nerve_sampler_step's. */
 int nerve_sampler_step_static_scratch(nerve_sampler *sampler, const nerve_sampler_batch *batch, void *stream);
 
+/* ---- LM head fused with the step (the projection's tile records) ----------------------
+ * A tile record is two words per batch row and per 64 vocabulary columns t:
+ * records[row*tile_stride + 2*t] = the largest order key of logits [64 t, 64 t + 64) (the
+ * float's bits mapped so that larger values give larger unsigned keys: non-negative x ->
+ * bits | 0x80000000, negative -> ~bits, +-0 -> 0x80000000, NaN excluded), and word
+ * 2*t + 1 = the count of NaNs among them. tile_stride counts records (>= ceil(vocab/64));
+ * the array holds batch x tile_stride x 8 bytes, 8-byte aligned. */
+
+/* logits[b*logits_row_stride + v] = output_scale * sum_d frames[b][d] * weight[v][d] for
+ * b < batch, v < vocab_size: bf16 frames [batch][frames_row_stride] and weight
+ * [vocab][weight_row_stride] (16-byte aligned, strides multiples of 8, input_size a
+ * multiple of 64), f32 accumulation and output; with tile_records, also the tile record of
+ * every row and 64 columns. Replaces tied_output_projection_batch_bf16.comp.template
+ * (dispatched by batched_output_projection.rs:162-206), whose per-lane summation order
+ * this does not reproduce (f32 sums of the same products in another order). */
+int nerve_lm_head_project(const void *frames, uint32_t frames_row_stride, const void *weight,
+                          uint32_t weight_row_stride, uint32_t batch, uint32_t input_size,
+                          uint32_t vocab_size, float output_scale, float *logits, uint32_t logits_row_stride,
+                          uint32_t *tile_records, uint32_t tile_stride, void *stream);
+
+/* The tile records of existing logits (dtype NERVE_DTYPE_F32 or NERVE_DTYPE_BF16), as the
+ * projection's epilogue writes them. No counterpart in the reference: for logits that
+ * another producer wrote. */
+int nerve_tile_records(const void *logits, uint32_t dtype, uint32_t logits_row_stride, uint32_t batch,
+                       uint32_t vocab_size, uint32_t *tile_records, uint32_t tile_stride, void *stream);
+
+/* nerve_sampler_step given the tile records of batch->logits: reads the records and only
+ * the tiles that can hold a survivor instead of every logit (sample_lanes,
+ * batched_output_projection.rs:316-371, after the projection). Results equal
+ * nerve_sampler_step's on the same logits; rows the records cannot narrow (fewer than
+ * top_k clean tiles, constant rows) read their whole row. One workgroup per row. */
+int nerve_sampler_step_tiles(nerve_sampler *sampler, const nerve_sampler_batch *batch,
+                             const uint32_t *tile_records, uint32_t tile_stride, void *stream);
+
 /* Sets bits for token ids < vocab_size into per-row seen bitmaps:
  * seen[row*seen_stride + id/32] |= 1 << (id%32) for ids[row*ids_stride + i], i < min(counts[row], max_count).
  * ids and counts are device arrays; max_count is the host-side bound of the call and must be

@@ -289,7 +289,8 @@ namespace {
 // One step; `static_scratch` takes the cross-workgroup scratch (used only when
 // a row has several slices) from the library's static per-GPU array instead
 // of the handle's allocation.
-int step_impl(nerve_sampler *s, const nerve_sampler_batch *b, void *stream, bool static_scratch) {
+int step_impl(nerve_sampler *s, const nerve_sampler_batch *b, void *stream, bool static_scratch,
+              const uint32_t *tile_records = nullptr, uint32_t tile_stride = 0u) {
     if (!s || !b) return fail(NERVE_ERR_INVALID_ARGUMENT, "null argument");
     const nerve_sampler_desc &d = s->desc;
     if (b->batch == 0u) return NERVE_OK;
@@ -324,6 +325,13 @@ int step_impl(nerve_sampler *s, const nerve_sampler_batch *b, void *stream, bool
     if (b->output_ring && !b->stream_control) return fail(NERVE_ERR_INVALID_ARGUMENT, "output_ring requires stream_control");
     if (b->output_ring && b->ring_stride < 4u) return fail(NERVE_ERR_INVALID_ARGUMENT, "ring_stride must hold the 4-word record");
 
+    const bool tiles = tile_records != nullptr;
+    if (tiles) {
+        const uint32_t ntiles = (d.vocab_size + nerve::tile_columns() - 1u) / nerve::tile_columns();
+        if (ntiles > nerve::max_tiles()) return fail(NERVE_ERR_INVALID_ARGUMENT, "vocabulary too large for tile records");
+        if (tile_stride < ntiles) return fail(NERVE_ERR_INVALID_ARGUMENT, "tile_stride < ceil(vocab/64)");
+        if ((uintptr_t)tile_records % 8u) return fail(NERVE_ERR_INVALID_ARGUMENT, "tile_records must be 8-byte aligned");
+    }
     const size_t esize = d.dtype == NERVE_DTYPE_F32 ? 4u : 2u;
     const bool aligned = ((uintptr_t)b->logits % 16u == 0u) && ((b->logits_row_stride * esize) % 16u == 0u);
     // 16-byte loads need an aligned row base and stride and at least one full slot.
@@ -335,9 +343,9 @@ int step_impl(nerve_sampler *s, const nerve_sampler_batch *b, void *stream, bool
     const uint32_t epv = nerve::elems_per_vector(variant);
     const uint32_t nvec = d.vocab_size / epv;  // full slots; the V % epv tail goes to the last slice
     const uint32_t per_slice_max = nerve::block_threads() * nerve::max_vectors_per_lane(variant);
-    uint32_t slices = d.slices_per_row ? s->slices : auto_slices(d, b->batch);
+    uint32_t slices = tiles ? 1u : (d.slices_per_row ? s->slices : auto_slices(d, b->batch));
     const uint32_t slices_need = (nvec + per_slice_max - 1u) / per_slice_max;
-    if (slices < slices_need) slices = slices_need;
+    if (slices < slices_need && !tiles) slices = slices_need;
     if (slices > s->slices_capacity) {
         char buf[200];
         std::snprintf(buf, sizeof(buf),
@@ -347,7 +355,7 @@ int step_impl(nerve_sampler *s, const nerve_sampler_batch *b, void *stream, bool
         return fail(NERVE_ERR_INVALID_ARGUMENT, buf);
     }
     const uint32_t vec_per_slice = (nvec + slices - 1u) / slices;
-    const uint32_t nv = nerve::vectors_per_lane(variant, (vec_per_slice + nerve::block_threads() - 1u) / nerve::block_threads());
+    const uint32_t nv = tiles ? 1u : nerve::vectors_per_lane(variant, (vec_per_slice + nerve::block_threads() - 1u) / nerve::block_threads());
     if (nv == 0u) return fail(NERVE_ERR_INVALID_ARGUMENT, "slice exceeds the kernel's register capacity");
 
     nerve::StepArgs a;
@@ -409,8 +417,23 @@ int step_impl(nerve_sampler *s, const nerve_sampler_batch *b, void *stream, bool
     a.feedback_stride = b->feedback_stride;
     a.stop_tokens = b->stop_tokens;
     a.stop_stride = b->stop_stride;
-    s->last_slices = slices;
     const size_t static_lds = 2u * 1024u;  // reduction scratch
+    if (tiles) {
+        a.tile_records = (const uint2 *)tile_records;
+        a.tile_stride = tile_stride;
+        a.dyn_lds_bytes = nerve::sample_tiles_lds_bytes(a.hash_slots, d.vocab_size, pen, d.top_k_capacity);
+        if (a.dyn_lds_bytes + static_lds + 6u * 1024u > s->lds_per_block)
+            return fail(NERVE_ERR_INVALID_ARGUMENT, "LDS need of the tile step (vocabulary, history, top_k_capacity) exceeds the device");
+        s->last_slices = 1u;
+        int prev_t = 0;
+        (void)hipGetDevice(&prev_t);
+        if (prev_t != s->device) (void)hipSetDevice(s->device);
+        const hipError_t et = nerve::launch_sample_tiles(d.dtype == NERVE_DTYPE_BF16, a, (hipStream_t)stream);
+        if (prev_t != s->device) (void)hipSetDevice(prev_t);
+        if (et != hipSuccess) return hip_fail(et, "sample_tiles launch");
+        return NERVE_OK;
+    }
+    s->last_slices = slices;
     if (stream_lds + static_lds > s->lds_per_block || a.finish_lds_bytes + static_lds > s->lds_per_block)
         return fail(NERVE_ERR_INVALID_ARGUMENT, "LDS need of this top_k_capacity / history / slice count exceeds the device");
 
@@ -461,6 +484,52 @@ int nerve_sampler_step(nerve_sampler *s, const nerve_sampler_batch *b, void *str
 
 int nerve_sampler_step_static_scratch(nerve_sampler *s, const nerve_sampler_batch *b, void *stream) {
     return step_impl(s, b, stream, true);
+}
+
+int nerve_sampler_step_tiles(nerve_sampler *s, const nerve_sampler_batch *b, const uint32_t *tile_records,
+                             uint32_t tile_stride, void *stream) {
+    if (!tile_records) return fail(NERVE_ERR_INVALID_ARGUMENT, "tile_records is required");
+    return step_impl(s, b, stream, false, tile_records, tile_stride);
+}
+
+int nerve_tile_records(const void *logits, uint32_t dtype, uint32_t logits_row_stride, uint32_t batch, uint32_t vocab_size,
+                       uint32_t *tile_records, uint32_t tile_stride, void *stream) {
+    if (batch == 0u) return NERVE_OK;
+    if (!logits || !tile_records) return fail(NERVE_ERR_INVALID_ARGUMENT, "null argument");
+    if (dtype != NERVE_DTYPE_F32 && dtype != NERVE_DTYPE_BF16) return fail(NERVE_ERR_INVALID_ARGUMENT, "dtype must be f32 or bf16");
+    if (vocab_size == 0u || logits_row_stride < vocab_size)
+        return fail(NERVE_ERR_INVALID_LOGITS_BYTE_CAPACITY, "logits_row_stride < vocab_size");
+    const uint32_t ntiles = (vocab_size + nerve::tile_columns() - 1u) / nerve::tile_columns();
+    if (tile_stride < ntiles) return fail(NERVE_ERR_INVALID_ARGUMENT, "tile_stride < ceil(vocab/64)");
+    if ((uintptr_t)tile_records % 8u) return fail(NERVE_ERR_INVALID_ARGUMENT, "tile_records must be 8-byte aligned");
+    const hipError_t e = nerve::launch_tile_records(dtype == NERVE_DTYPE_BF16, logits, logits_row_stride, batch, vocab_size,
+                                                    (uint2 *)tile_records, tile_stride, (hipStream_t)stream);
+    return e == hipSuccess ? NERVE_OK : hip_fail(e, "tile_records launch");
+}
+
+int nerve_lm_head_project(const void *frames, uint32_t frames_row_stride, const void *weight, uint32_t weight_row_stride,
+                          uint32_t batch, uint32_t input_size, uint32_t vocab_size, float output_scale, float *logits,
+                          uint32_t logits_row_stride, uint32_t *tile_records, uint32_t tile_stride, void *stream) {
+    if (batch == 0u || vocab_size == 0u) return NERVE_OK;
+    if (!frames || !weight || !logits) return fail(NERVE_ERR_INVALID_ARGUMENT, "null argument");
+    if (input_size == 0u || input_size % 64u)
+        return fail(NERVE_ERR_INVALID_ARGUMENT, "input_size must be a positive multiple of 64");
+    if (frames_row_stride < input_size || weight_row_stride < input_size || frames_row_stride % 8u || weight_row_stride % 8u)
+        return fail(NERVE_ERR_INVALID_ARGUMENT, "frame and weight row strides must be >= input_size and multiples of 8");
+    if ((uintptr_t)frames % 16u || (uintptr_t)weight % 16u)
+        return fail(NERVE_ERR_INVALID_ARGUMENT, "frames and weight must be 16-byte aligned");
+    if (logits_row_stride < vocab_size) return fail(NERVE_ERR_INVALID_LOGITS_BYTE_CAPACITY, "logits_row_stride < vocab_size");
+    if ((uint64_t)(batch < 256u ? batch : 256u) * frames_row_stride * 2u >= (1ull << 31) ||
+        (uint64_t)128u * weight_row_stride * 2u >= (1ull << 31))
+        return fail(NERVE_ERR_INVALID_ARGUMENT, "row strides too large");
+    const uint32_t ntiles = (vocab_size + nerve::tile_columns() - 1u) / nerve::tile_columns();
+    if (tile_records && tile_stride < ntiles) return fail(NERVE_ERR_INVALID_ARGUMENT, "tile_stride < ceil(vocab/64)");
+    if (tile_records && (uintptr_t)tile_records % 8u) return fail(NERVE_ERR_INVALID_ARGUMENT, "tile_records must be 8-byte aligned");
+    if (!(output_scale - output_scale == 0.0f)) return fail(NERVE_ERR_INVALID_ARGUMENT, "output_scale must be finite");
+    const hipError_t e = nerve::launch_lm_head((const uint16_t *)frames, frames_row_stride, (const uint16_t *)weight,
+                                               weight_row_stride, batch, input_size, vocab_size, output_scale, logits,
+                                               logits_row_stride, (uint2 *)tile_records, tile_stride, (hipStream_t)stream);
+    return e == hipSuccess ? NERVE_OK : hip_fail(e, "lm_head launch");
 }
 
 int nerve_sampler_record_tokens(nerve_sampler *s, uint32_t *seen, uint32_t seen_stride, uint32_t rows,

@@ -64,6 +64,8 @@ struct StepArgs {
     uint32_t feedback_stride;
     const uint32_t *stop_tokens;
     uint32_t stop_stride;
+    const uint2 *tile_records;  // [batch][tile_stride] {largest order key, NaN count} per 64 columns
+    uint32_t tile_stride;
 };
 
 // Bytes of the static scratch array of nerve_sampler_step_static_scratch
@@ -97,6 +99,17 @@ hipError_t launch_rows_scalar_bf16_plain(const StepArgs &a, hipStream_t stream);
 hipError_t launch_rows_scalar_bf16_mask(const StepArgs &a, hipStream_t stream);
 hipError_t launch_rows_scalar_f32_plain(const StepArgs &a, hipStream_t stream);
 hipError_t launch_rows_scalar_f32_mask(const StepArgs &a, hipStream_t stream);
+// sampling from tile records (nerve_tiles.hip)
+hipError_t launch_sample_tiles(bool bf16, const StepArgs &a, hipStream_t stream);
+uint32_t sample_tiles_lds_bytes(uint32_t hash_slots, uint32_t vocab, bool pen, uint32_t kcap);
+uint32_t tile_columns();
+uint32_t max_tiles();
+hipError_t launch_tile_records(bool bf16, const void *logits, uint64_t ld, uint32_t batch, uint32_t vocab, uint2 *records,
+                               uint32_t rec_stride, hipStream_t stream);
+// LM-head projection with the tile-record epilogue (nerve_lm_head.hip)
+hipError_t launch_lm_head(const uint16_t *frames, uint64_t frames_ld, const uint16_t *weight, uint64_t weight_ld,
+                          uint32_t batch, uint32_t input_size, uint32_t vocab, float scale, float *logits, uint64_t logits_ld,
+                          uint2 *records, uint32_t rec_stride, hipStream_t stream);
 hipError_t launch_record_tokens(uint32_t *seen, uint32_t seen_stride, uint32_t rows, const uint32_t *ids,
                                 uint32_t ids_stride, const uint32_t *counts, uint32_t max_count, uint32_t vocab,
                                 hipStream_t stream);

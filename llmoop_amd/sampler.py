@@ -173,7 +173,12 @@ EXPORTED_SYMBOLS = (
     "nerve_sampler_last_error",
     "nerve_sampler_abi_version",
     "nerve_sampler_slices_per_row",
+    "nerve_sampler_step_tiles",
+    "nerve_tile_records",
+    "nerve_lm_head_project",
 )
+
+TILE_COLUMNS = 64  # vocabulary columns per tile record
 
 _lib = None
 
@@ -201,6 +206,9 @@ def load_library() -> ctypes.CDLL:
     lib.nerve_sampler_abi_version.restype = u32
     lib.nerve_sampler_slices_per_row.restype = u32
     lib.nerve_sampler_slices_per_row.argtypes = [P]
+    lib.nerve_sampler_step_tiles.argtypes = [P, P, P, u32, P]
+    lib.nerve_tile_records.argtypes = [P, u32, u32, u32, u32, P, u32, P]
+    lib.nerve_lm_head_project.argtypes = [P, u32, P, u32, u32, u32, u32, ctypes.c_float, P, u32, P, u32, P]
     _lib = lib
     return lib
 
@@ -371,7 +379,8 @@ class Sampler:
              eos_token_id: int = 2, seeds=None, steps=None, rng: int = RNG_REFERENCE_HASH, stream_control=None,
              output_ring=None, topk_ids=None, topk_logits=None, topk_probs=None, stream=None, flags: int = 0,
              tick_base: int = 0, seen_shared: bool = False, prefix_ids=None, prefix_counts=None,
-             feedback_control=None, stop_tokens=None, entry: str = "nerve_sampler_step") -> None:
+             feedback_control=None, stop_tokens=None, entry: str = "nerve_sampler_step",
+             tile_records=None) -> None:
         """Launches one step. All array arguments are torch tensors on the device:
         logits [B, stride] (float32, or bfloat16/int16 bits), params uint8 [B*32] holding ROW_PARAMS records,
         out int32 [B, 4], optional history int32 [B, H] + history_len int32 [B], seen / allowed int32 [B, W]
@@ -379,7 +388,9 @@ class Sampler:
         stream_control int32 [B, 5], output_ring int32 [B, R], topk_* [B, top_k_capacity];
         prefix_ids int32 [B, P] with prefix_counts int32 [B], or [n] without counts (row r takes ids[:r+1]);
         feedback_control int32 [B, F] or [F] (one block for every row), stop_tokens int32 [B, W] or [W].
-        `entry` selects the C entry point (nerve_sampler_step or nerve_sampler_step_static_scratch)."""
+        `entry` selects the C entry point (nerve_sampler_step or nerve_sampler_step_static_scratch);
+        tile_records int32 [B, 2 * ceil(V/64) or more] (the projection's records of these logits)
+        selects nerve_sampler_step_tiles."""
         b = _Batch()
         logits, lstride = _rows(logits)
         B = logits.shape[0]
@@ -430,6 +441,11 @@ class Sampler:
         if stop_tokens is not None:
             b.stop_tokens = stop_tokens.data_ptr()
             b.stop_stride = 0 if stop_tokens.dim() == 1 else _rows(stop_tokens)[1]
+        if tile_records is not None:
+            recs, rstride = _rows(tile_records)
+            _check(load_library().nerve_sampler_step_tiles(self._h, ctypes.byref(b), recs.data_ptr(), rstride // 2,
+                                                           _stream_arg(stream, self.device)))
+            return
         _check(getattr(load_library(), entry)(self._h, ctypes.byref(b), _stream_arg(stream, self.device)))
 
     def record_tokens(self, seen, ids, counts, max_count: int, stream=None) -> None:
@@ -639,3 +655,44 @@ class SamplerRunner:
         cap = self.history_capacity if dynamic_state_capacity_activations is None else dynamic_state_capacity_activations
         ticks = [start_stream_tick + i for i in range(n)]
         return self.sample_lanes(logits, [list(input_token_ids[: i + 1]) for i in range(n)], ticks, [cap] * n)
+
+
+# ---- LM head fused with the step --------------------------------------------------
+
+
+def tile_count(vocab: int) -> int:
+    return (vocab + TILE_COLUMNS - 1) // TILE_COLUMNS
+
+
+def lm_head_project(frames, weight, logits, *, output_scale: float = 1.0, tile_records=None, stream=None) -> None:
+    """logits[b, v] = output_scale * frames[b] . weight[v] (tied_output_projection_batch_bf16.comp.template):
+    frames [B, D] and weight [V, D] bfloat16 (or int16 bits) on the device, logits float32 [B, >= V];
+    tile_records int32 [B, >= 2 * ceil(V/64)] receives the tile records when given."""
+    frames, fs = _rows(frames)
+    weight, ws = _rows(weight)
+    logits, ls = _rows(logits)
+    B, D = frames.shape[0], frames.shape[1]
+    V = weight.shape[0]
+    if weight.shape[1] != D:
+        raise ValueError("frames and weight disagree on input_size")
+    rp, rs = 0, 0
+    if tile_records is not None:
+        tr, trs = _rows(tile_records)
+        rp, rs = tr.data_ptr(), trs // 2
+    dev = frames.device.index or 0
+    _check(load_library().nerve_lm_head_project(frames.data_ptr(), fs, weight.data_ptr(), ws, B, D, V,
+                                                float(output_scale), logits.data_ptr(), ls, rp or None, rs,
+                                                _stream_arg(stream, dev)))
+
+
+def tile_records(logits, records, *, vocab: int | None = None, stream=None) -> None:
+    """The tile records of existing logits (float32, or bfloat16 / int16 bits) into records int32 [B, >= 2 * tiles]."""
+    import torch
+
+    lg, ls = _rows(logits)
+    dtype = DTYPE_F32 if lg.dtype == torch.float32 else DTYPE_BF16
+    V = ls if vocab is None else vocab
+    tr, trs = _rows(records)
+    dev = lg.device.index or 0
+    _check(load_library().nerve_tile_records(lg.data_ptr(), dtype, ls, lg.shape[0], V, tr.data_ptr(), trs // 2,
+                                             _stream_arg(stream, dev)))

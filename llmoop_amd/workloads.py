@@ -92,9 +92,21 @@ def _mask(rng, B, V, empty_rows):
     return w.astype(np.uint32)
 
 
-def make(name: str, seed: int = 1234, step: int = 0, batch: int | None = None) -> Workload:
+def make(name: str, seed: int = 1234, step: int = 0, batch: int | None = None, input_size: int = 4096) -> Workload:
     rng = np.random.default_rng(seed)
     name = name.upper()
+    if name == "L5":
+        # C5's sampling settings on logits from an LM-head projection: frames
+        # [B, input_size] bf16 ~ N(0, 1), weight [V, input_size] bf16 ~ N(0, 0.04^2),
+        # made on the device by lm_head_inputs(); float32 logits, std ~ 0.04 sqrt(input_size)
+        w = make("C5", seed=seed, step=step, batch=batch)
+        w.name = "L5"
+        w.dtype = "f32"
+        w.logits = None
+        w.extra.update(input_size=input_size, scale=1.0, seed=seed)
+        w.description = (f"LM head + step: B={w.batch}, input_size={input_size}, V={w.vocab}, bf16 frames and weight, "
+                         "f32 logits, C5's penalties and sampling")
+        return w
     if name == "C1":
         B, V = batch or 1, 32000
         x = (rng.standard_normal((B, V)) * 2.0).astype(np.float32)
@@ -147,3 +159,18 @@ def make(name: str, seed: int = 1234, step: int = 0, batch: int | None = None) -
                         description="large-batch decode: B=256, V=151936, bf16 Student-t, H=2048, per-row T"
                         + (", history from each row's own top 200" if name == "C5P" else ""))
     raise ValueError(f"unknown workload {name}")
+
+
+def lm_head_inputs(w: Workload, device):
+    """Seeded bf16 frames [B, D] and weight [V, D] of an L5 workload, made on the device."""
+    import torch
+
+    g = torch.Generator(device=device)
+    g.manual_seed(int(w.extra["seed"]))
+    D = int(w.extra["input_size"])
+    frames = torch.randn((w.batch, D), generator=g, device=device, dtype=torch.float32).to(torch.bfloat16)
+    weight = torch.empty((w.vocab, D), device=device, dtype=torch.bfloat16)
+    for v0 in range(0, w.vocab, 16384):  # in chunks: the float32 staging stays small
+        v1 = min(w.vocab, v0 + 16384)
+        weight[v0:v1] = (torch.randn((v1 - v0, D), generator=g, device=device) * 0.04).to(torch.bfloat16)
+    return frames, weight

@@ -23,7 +23,7 @@ def to_dev(a, dev, torch):
 
 def run_gpu(logits, params, *, top_k_capacity, history=None, history_len=None, seen=None, allowed=None,
             seeds=None, steps=None, rng=S.RNG_REFERENCE_HASH, eos_token_id=2, slices_per_row=0, sampler=None,
-            vocab=None):
+            vocab=None, tiles=False, prefix_ids=None, prefix_counts=None):
     import torch
 
     dev = torch.device("cuda:0")
@@ -45,7 +45,16 @@ def run_gpu(logits, params, *, top_k_capacity, history=None, history_len=None, s
     tpr = torch.zeros((B, kcap), dtype=torch.float32, device=dev)
     if history is not None and history_len is None:
         history_len = np.full(B, H, np.uint32)
-    sampler.step(lg, S.params_tensor(params, dev), out, history=to_dev(history, dev, torch),
+    kw = {}
+    if tiles:
+        # the tile records of these logits (as the projection's epilogue writes them), then the tile step
+        rec = torch.full((B, 2 * S.tile_count(V) + 2), -1, dtype=torch.int32, device=dev)
+        S.tile_records(lg, rec, vocab=V)
+        kw["tile_records"] = rec
+    if prefix_ids is not None:
+        kw["prefix_ids"] = to_dev(prefix_ids, dev, torch)
+        kw["prefix_counts"] = to_dev(prefix_counts, dev, torch)
+    sampler.step(lg, S.params_tensor(params, dev), out, **kw, history=to_dev(history, dev, torch),
                  history_len=to_dev(history_len, dev, torch), seen=to_dev(seen, dev, torch),
                  allowed=to_dev(allowed, dev, torch), eos_token_id=eos_token_id, seeds=to_dev(seeds, dev, torch),
                  steps=to_dev(steps, dev, torch), rng=rng, topk_ids=tid, topk_logits=tlg, topk_probs=tpr)

@@ -21,7 +21,7 @@ def S():
 
 def test_header_symbols_are_exported(S):
     header = open(os.path.join(ROOT, "include", "nerve_sampler.h")).read()
-    declared = set(re.findall(r"^\s*(?:int|uint32_t|const char \*)\s*(nerve_sampler_\w+)\s*\(", header, re.M))
+    declared = set(re.findall(r"^\s*(?:int|uint32_t|const char \*)\s*(nerve_\w+)\s*\(", header, re.M))
     assert declared, "no declarations parsed"
     assert declared == set(S.EXPORTED_SYMBOLS)
     lib = S.load_library()
