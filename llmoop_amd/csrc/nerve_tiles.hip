@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void tile_records_kernel(const Elem *logits, u
 // LDS of sample_tiles_kernel, in layout order.
 __host__ __device__ constexpr uint32_t tiles_lds_bytes(uint32_t hash_slots, uint32_t pen_words, uint32_t ntiles,
                                                        uint32_t kcap) {
-    return hash_slots * 4u + pen_words * 4u + ntiles * 4u + kTileCandCap * 4u + kStreamCandCap * 8u + kcap * 8u +
+    return hash_slots * 4u + pen_words * 4u + ntiles * 8u + kTileCandCap * 4u + kStreamCandCap * 8u + kcap * 8u +
            kcap * 8u;
 }
 
@@ -72,11 +72,15 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
     const uint32_t ntiles = (V + kTileCols - 1u) / kTileCols;
     const uint32_t words = (V + 31u) / 32u;
     const uint32_t pen_words = PEN != 0 ? words : 0u;
-    uint32_t *s_hash = s_dyn;                                   // [hash_slots] id -> count
+    uint32_t *s_hash = s_dyn;                                   // [hash_slots] id -> repeats (occurrences past the first)
     uint32_t *s_pen = s_hash + a.hash_slots;                    // [pen_words] penalised ids of the row
     uint32_t *s_ck = s_pen + pen_words;                         // [ntiles] record key of clean tiles, else 0
-    uint32_t *s_ct = s_ck + ntiles;                             // [kTileCandCap] candidate tiles
-    uint64_t *s_cand = (uint64_t *)(((uintptr_t)(s_ct + kTileCandCap) + 7u) & ~(uintptr_t)7u);  // [kStreamCandCap]
+    uint32_t *s_rk = s_ck + ntiles;                             // [ntiles] record key of every tile
+    uint32_t *s_ct = s_rk + ntiles;                             // [kTileCandCap] candidate tiles
+    // 8-byte aligned by index arithmetic on s_dyn (a cast through an integer
+    // would lose the LDS address space and turn every access into a flat one)
+    const uint32_t cand_off = (a.hash_slots + pen_words + 2u * ntiles + kTileCandCap + 1u) & ~1u;
+    uint64_t *s_cand = (uint64_t *)(s_dyn + cand_off);          // [kStreamCandCap]
     uint2 *s_sorted = (uint2 *)(s_cand + kStreamCandCap);       // [kcap]
     float *s_w = (float *)(s_sorted + a.kcap);                  // [kcap]
     float *s_p = s_w + a.kcap;                                  // [kcap]
@@ -87,6 +91,30 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
     const Elem *lrow = (const Elem *)a.logits + (uint64_t)row * a.ld;
     const uint32_t *arow = MASK ? a.allowed + (uint64_t)row * a.allowed_stride : nullptr;
     const uint2 *rec = a.tile_records + (uint64_t)row * a.tile_stride;
+    // every load that depends on nothing is issued first: the tile records
+    // and mask word pairs of this lane (tile t = tid + 512 u, u < 8; ntiles
+    // <= 4096) and its history ids (up to the stride; the length masks them
+    // later), so their latencies overlap
+    uint2 r[8];
+    uint2 mw[MASK ? 8 : 1];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const uint32_t t = tid + (uint32_t)u * kBlock;
+        r[u] = t < ntiles ? rec[t] : make_uint2(0u, 0u);
+        if constexpr (MASK) {
+            const uint32_t w0 = 2u * t, w1 = w0 + 1u;
+            mw[u] = make_uint2(t < ntiles ? arow[w0] : 0u, w1 < words && t < ntiles ? arow[w1] : 0u);
+        }
+    }
+    uint32_t hid[PEN == 2 ? 8 : 1];
+    if constexpr (PEN == 2) {
+        const uint32_t *hrow = a.history + (uint64_t)row * a.history_stride;
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+            const uint32_t i = tid + (uint32_t)h * kBlock;
+            hid[h] = i < a.history_stride ? hrow[i] : 0xffffffffu;
+        }
+    }
     const nerve_sampler_row_params P = a.params[row];
     const RowIo io = load_row_io(a, row);
     const bool sampled = P.method != NERVE_METHOD_GREEDY;
@@ -97,7 +125,7 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
     const bool lowering = P.repetition_penalty >= 1.0f && P.frequency_penalty >= 0.0f && P.presence_penalty >= 0.0f;
 
     // 1. penalty state: the row's penalised ids as an LDS bitmap, and (history)
-    // every id's count in the table
+    // the repeats of each id in the table
     if (tid == 0) {
         sm.flag[0] = 0u;  // candidate tiles
         sm.flag[1] = 0u;  // candidates
@@ -109,20 +137,32 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
         lds_sync();
         uint32_t len = a.history_len[row];
         len = len > a.history_stride ? a.history_stride : len;
-        const uint32_t *hrow = a.history + (uint64_t)row * a.history_stride;
-        for (uint32_t i = tid; i < len; i += kBlock) {
-            const uint32_t id = hrow[i];
-            if (id < V) {
-                atomicOr(&s_pen[id >> 5], 1u << (id & 31u));
-                hash_insert(s_hash, a.log2_slots, id);
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+            const uint32_t id = hid[h];
+            if (tid + (uint32_t)h * kBlock < len && id < V) {
+                // the bitmap holds first occurrences; the table only repeats
+                // (short probe chains: a wave waits for its longest one)
+                const uint32_t bit = 1u << (id & 31u);
+                if (atomicOr(&s_pen[id >> 5], bit) & bit) hash_insert(s_hash, a.log2_slots, id);
             }
         }
     } else if constexpr (PEN == 1) {
         const uint32_t *srow = a.seen + (uint64_t)row * a.seen_stride;
-        for (uint32_t i = tid; i < words; i += kBlock) {
-            uint32_t w = srow[i];
-            if (i == words - 1u && (V & 31u)) w &= (1u << (V & 31u)) - 1u;
-            s_pen[i] = w;
+        for (uint32_t i0 = tid; i0 < words; i0 += 8u * kBlock) {
+            uint32_t sw[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t i = i0 + (uint32_t)u * kBlock;
+                sw[u] = i < words ? srow[i] : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t i = i0 + (uint32_t)u * kBlock;
+                uint32_t w = sw[u];
+                if (i == words - 1u && (V & 31u)) w &= (1u << (V & 31u)) - 1u;
+                if (i < words) s_pen[i] = w;
+            }
         }
         const uint32_t np = prefix_count(a, row);
         lds_sync();
@@ -142,7 +182,7 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
         uint32_t key = raw_order_key(bits);
         if constexpr (PEN != 0) {
             if ((s_pen[id >> 5] >> (id & 31u)) & 1u) {
-                const uint32_t count = PEN == 2 ? hash_lookup(s_hash, a.log2_slots, id) : 1u;
+                const uint32_t count = PEN == 2 ? 1u + hash_lookup(s_hash, a.log2_slots, id) : 1u;
                 key = order_key(configured_logit(u2f(bits), true, count, P.repetition_penalty, P.frequency_penalty,
                                                  P.presence_penalty));
             }
@@ -152,24 +192,31 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
 
     // 2. records: clean keys to LDS, the lane's largest clean key, the row's
     // NaN and allowed flags
+    // every record (and mask pair) of this lane loaded before any is used:
+    // tile t = tid + 512 u, u < 8 (ntiles <= 4096)
     uint32_t best = 0u, any_allowed = MASK ? 0u : 1u, nan_count = 0u;
-    for (uint32_t t = tid; t < ntiles; t += kBlock) {
-        const uint2 r = rec[t];
-        nan_count += r.y;
-        const uint32_t w0 = 2u * t, w1 = w0 + 1u;
-        bool clean = (t + 1u) * kTileCols <= V;  // a partial last tile is never clean
-        if constexpr (PEN != 0) clean = clean && s_pen[w0] == 0u && (w1 >= words || s_pen[w1] == 0u);
-        if constexpr (MASK) {
-            uint32_t m0 = arow[w0], m1 = w1 < words ? arow[w1] : 0u;
-            if (w0 == words - 1u && (V & 31u)) m0 &= (1u << (V & 31u)) - 1u;
-            if (w1 == words - 1u && (V & 31u)) m1 &= (1u << (V & 31u)) - 1u;
-            any_allowed |= (m0 | m1) ? 1u : 0u;
-            clean = clean && m0 == 0xffffffffu && m1 == 0xffffffffu;
+    {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t t = tid + (uint32_t)u * kBlock;
+            if (t >= ntiles) continue;
+            nan_count += r[u].y;
+            const uint32_t w0 = 2u * t, w1 = w0 + 1u;
+            bool clean = (t + 1u) * kTileCols <= V;  // a partial last tile is never clean
+            if constexpr (PEN != 0) clean = clean && s_pen[w0] == 0u && (w1 >= words || s_pen[w1] == 0u);
+            if constexpr (MASK) {
+                uint32_t m0 = mw[u].x, m1 = mw[u].y;
+                if (w0 == words - 1u && (V & 31u)) m0 &= (1u << (V & 31u)) - 1u;
+                if (w1 == words - 1u && (V & 31u)) m1 &= (1u << (V & 31u)) - 1u;
+                any_allowed |= (m0 | m1) ? 1u : 0u;
+                clean = clean && m0 == 0xffffffffu && m1 == 0xffffffffu;
+            }
+            const uint32_t key = r[u].x < valid_min ? 0u : r[u].x;
+            s_rk[t] = r[u].x;
+            const uint32_t ck = clean ? key : 0u;
+            s_ck[t] = ck;
+            best = max(best, ck);
         }
-        const uint32_t key = r.x < valid_min ? 0u : r.x;
-        const uint32_t ck = clean ? key : 0u;
-        s_ck[t] = ck;
-        best = max(best, ck);
     }
     {
         const uint32_t f = (__ballot(any_allowed != 0u) ? 1u : 0u) | (__ballot(nan_count != 0u) ? 4u : 0u);
@@ -181,7 +228,7 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
     uint32_t thr;
     if (k <= 64u) {
         const uint32_t b1[1] = {best};
-        const uint32_t tw = wave_kth<1, 24>(b1, k);
+        const uint32_t tw = wave_kth<1, 16>(b1, k);
         const bool in = best != 0u && best >= tw;
         const uint64_t bal = __ballot(in);
         const uint32_t pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
@@ -192,7 +239,7 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
             uint32_t uk[kWaves];
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) uk[w] = lane < sm.ucount[0][w] ? sm.ukeys[0][w * 64 + lane] : 0u;
-            const uint32_t t = wave_kth<kWaves, 24>(uk, k);
+            const uint32_t t = wave_kth<kWaves, 16>(uk, k);
             if (lane == 0u) sm.uthr[0] = t;
         }
         lds_sync();
@@ -209,7 +256,7 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
     // 4. candidate tiles, then their elements
     if (!exact) {
         for (uint32_t t = tid; t < ntiles; t += kBlock) {
-            const uint32_t key = rec[t].x;
+            const uint32_t key = s_rk[t];
             if (key >= thr) {
                 const uint32_t q = atomicAdd(&sm.flag[0], 1u);
                 if (q < kTileCandCap) s_ct[q] = t;
@@ -225,17 +272,17 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
                 const uint32_t q = atomicAdd(&sm.flag[1], 1u);
                 if (q < kStreamCandCap) s_cand[q] = cand_pack(key, id);
             };
-            // 8 elements per lane and round, every load issued before any key
-            for (uint32_t e0 = tid; e0 < nel; e0 += 8u * kBlock) {
-                uint32_t bits[8], ids[8];
+            // 16 elements per lane and round, every load issued before any key
+            for (uint32_t e0 = tid; e0 < nel; e0 += 16u * kBlock) {
+                uint32_t bits[16], ids[16];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
+                for (int u = 0; u < 16; ++u) {
                     const uint32_t e = e0 + (uint32_t)u * kBlock;
                     ids[u] = e < nel ? s_ct[e / kTileCols] * kTileCols + (e % kTileCols) : 0xffffffffu;
                     bits[u] = ids[u] < V ? f2u(load_elem<Elem>(lrow, ids[u])) : 0u;
                 }
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
+                for (int u = 0; u < 16; ++u) {
                     const uint32_t id = ids[u];
                     if (id >= V) continue;
                     const uint32_t raw = raw_order_key(bits[u]);
@@ -325,7 +372,7 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
     ctx.allowed_row = arow;
     ctx.seen_row = PEN == 1 ? a.seen + (uint64_t)row * a.seen_stride : nullptr;
     ctx.hash = s_hash;
-    ctx.bitmap = PEN == 1 ? s_pen : nullptr;  // history: the table holds full counts
+    ctx.bitmap = PEN != 0 ? s_pen : nullptr;  // history: bitmap + the table of repeats
     ctx.log2_slots = a.log2_slots;
     ctx.tok0 = 0u;
     ctx.rep = P.repetition_penalty;
@@ -334,14 +381,29 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
     ctx.history = PEN == 2;
     ctx.prefix = nullptr;
     ctx.prefix_n = 0u;
-    for (uint32_t i = tid; i < C; i += kBlock) {
-        const uint64_t e = list[i];
-        uint32_t r = 0;
-        for (uint32_t j = 0; j < C; ++j) r += list[j] > e ? 1u : 0u;
-        if (r < k) {
+    // rank sort: 4 adjacent lanes per candidate, each counting the better
+    // entries among every 4th one (8 reads in flight), the counts summed
+    // across the 4 lanes (ids are distinct, so ranks are a permutation)
+    for (uint32_t base = 0; base < C; base += kBlock / 4u) {
+        const uint32_t i = base + (tid >> 2), part = tid & 3u;
+        const uint64_t e = i < C ? list[i] : 0u;
+        uint32_t rk = 0;
+        for (uint32_t j0 = part; j0 < C; j0 += 32u) {
+            uint64_t o[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const uint32_t j = j0 + 4u * (uint32_t)q;
+                o[q] = j < C ? list[j] : 0u;
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) rk += o[q] > e ? 1u : 0u;
+        }
+        rk += (uint32_t)__shfl_xor((int)rk, 1, 64);
+        rk += (uint32_t)__shfl_xor((int)rk, 2, 64);
+        if (part == 0u && i < C && rk < k) {
             uint2 en = cand_entry(e);
             if (en.x == kZeroKey && f2u(configured_at<Elem>(ctx, en.y)) == 0x80000000u) en.y |= kNegZeroFlag;
-            s_sorted[r] = en;
+            s_sorted[rk] = en;
         }
     }
     lds_sync();
@@ -354,8 +416,8 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
     const float u = sampled ? random_unit(a.rng, io.seed, (uint64_t)io.tick_lo | ((uint64_t)io.tick_hi << 32), row) : 0.0f;
     // the finish's NaN replay recomputes configured values over the whole row
     RowCtx fctx = ctx;
+    fctx.bitmap = nullptr;  // the replay rebuilds the table with full counts (history)
     if constexpr (PEN == 1) {
-        fctx.bitmap = nullptr;
         fctx.prefix = a.prefix_ids ? a.prefix_ids + (uint64_t)row * a.prefix_stride : nullptr;
         fctx.prefix_n = prefix_count(a, row);
     }
