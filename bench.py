@@ -48,7 +48,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", default="C5", help="C1..C5, C5P (C5 is the headline workload)")
+    ap.add_argument("--config", default="C5",
+                    help="C1..C5, C5P (C5 is the headline workload); L5: LM-head projection + step")
+    ap.add_argument("--input-size", type=int, default=4096, help="L5: width of the projected frames")
     ap.add_argument("--buffers", type=int, default=4, help="logits copies the steps rotate over")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
@@ -100,8 +102,116 @@ def measured_traffic(workload: str):
     return int(m.group(1)) if m else None
 
 
+def main_l5(args):
+    """L5: one decode tail = the LM-head projection (bf16 frames x bf16 weight
+    -> f32 logits, with the tile-record epilogue) then the step that samples
+    from the records. The same step through the projection without records
+    and the dense step, and each kernel alone, are timed beside it."""
+    import torch
+
+    from llmoop_amd import sampler as S
+    from llmoop_amd import workloads
+
+    dev = torch.device("cuda:0")
+    w = workloads.make("L5", seed=2024, step=0, input_size=args.input_size)
+    B, V, D = w.batch, w.vocab, args.input_size
+    frames, weight = workloads.lm_head_inputs(w, dev)
+    sampler = S.Sampler(V, B, dtype="f32", top_k_capacity=w.top_k_capacity, history_capacity=w.history.shape[1])
+
+    def dev_arr(a):
+        a = np.ascontiguousarray(a)
+        view = {np.uint32: np.int32, np.uint16: np.int16, np.uint64: np.int64}.get(a.dtype.type, a.dtype.type)
+        return torch.from_numpy(a.view(view).copy()).to(dev)
+
+    logits = torch.empty((B, V), dtype=torch.float32, device=dev)
+    records = torch.empty((B, 2 * S.tile_count(V)), dtype=torch.int32, device=dev)
+    params = S.params_tensor(w.params, dev)
+    kw = dict(history=dev_arr(w.history), history_len=dev_arr(w.history_len), seeds=dev_arr(w.seeds), rng=w.rng)
+    sc = torch.zeros((B, 5), dtype=torch.int32, device=dev)
+    out = torch.zeros((B, 4), dtype=torch.int32, device=dev)
+    scale = float(w.extra["scale"])
+
+    def project(rec=True):
+        S.lm_head_project(frames, weight, logits, output_scale=scale, tile_records=records if rec else None)
+
+    def fused():
+        project()
+        sampler.step(logits, params, out, stream_control=sc, tile_records=records, **kw)
+
+    def unfused():
+        project(False)
+        sampler.step(logits, params, out, stream_control=sc, **kw)
+
+    def timed(fn, n):
+        for _ in range(min(args.warmup, 10)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n, e0.elapsed_time(e1) / 1e3 / n
+
+    n = max(1, args.steps)
+    sc.zero_()
+    wall, dev_s = timed(fused, n)
+    ticks_done = int(sc[0, 1].item())
+    parity = None
+    if not args.no_check:
+        from oracle import oracle
+
+        ref = oracle.sample(logits.cpu().numpy(), w.params, top_k_capacity=w.top_k_capacity, history=w.history,
+                            history_len=w.history_len, seeds=w.seeds, steps=np.full(B, ticks_done - 1, np.uint64),
+                            rng=w.rng, threads=min(os.cpu_count() or 1, 16))
+        bad = int((out.cpu().numpy().view(np.uint32) != ref["out"]).any(axis=1).sum())
+        parity = {"rows_checked": B, "rows_mismatched": bad, "tick": ticks_done - 1, "checker": "oracle (CPU)"}
+        if bad:
+            print(json.dumps({"parity": parity}), flush=True)
+            sys.exit(f"bench.py: {bad} of {B} rows of the last fused step differ from the oracle")
+    _, unfused_s = timed(unfused, n)
+    _, proj_s = timed(project, n)
+    _, proj_norec_s = timed(lambda: project(False), n)
+    _, tiles_s = timed(lambda: sampler.step(logits, params, out, stream_control=sc, tile_records=records, **kw), n)
+    _, dense_s = timed(lambda: sampler.step(logits, params, out, stream_control=sc, **kw), n)
+    # the projection's once-through bytes: weight and frames read, logits and records written
+    proj_bytes = V * D * 2 + B * D * 2 + B * V * 4 + B * S.tile_count(V) * 8
+    flops = 2.0 * B * V * D
+    achieved = proj_bytes / proj_s / 1e9
+    res = {
+        "metric": "sampled rows/sec of LM head + sampling step (B=256, V=151936)",
+        "value": B / wall,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": n,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3,
+        "us_per_step": wall * 1e6,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16 x bf16 -> f32 projection, f32 sampling",
+        "data": "synthetic (random bf16 frames and weight made on the device)",
+        "config": {"workload": f"L5: {w.description}", "batch": B, "vocab": V, "input_size": D,
+                   "parallelism": "single GPU"},
+        "device_us": {"fused_step": dev_s * 1e6, "unfused_step": unfused_s * 1e6,
+                      "projection_with_records": proj_s * 1e6, "projection": proj_norec_s * 1e6,
+                      "tile_step": tiles_s * 1e6, "dense_step": dense_s * 1e6},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "lm_head_kernel",
+                     "algorithmic_bytes": proj_bytes, "mfma_tflops": flops / proj_s / 1e12,
+                     "mfma_frac_of_2500": flops / proj_s / 1e12 / 2500.0},
+        "parity": parity,
+    }
+    print(json.dumps(res), flush=True)
+
+
 def main():
     args = parse()
+    if args.config.upper() == "L5" and args.gpus == 1:
+        return main_l5(args)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(rows are independent: B rows shard over GPUs with no exchange)", file=sys.stderr)

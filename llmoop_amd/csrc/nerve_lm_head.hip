@@ -10,7 +10,7 @@
 // v_mfma_f32_32x32x16_bf16: wave w owns the 64 x 64 sub-block (w % 4, w / 4),
 // 2 x 2 MFMA tiles of 32 x 32 (64 accumulators per lane). The reduction
 // dimension goes through LDS 64 columns at a time, double-buffered, with the
-// global loads of a stage issued two stages ahead (16-byte buffer loads; rows
+// global loads of a stage issued several stages ahead (16-byte buffer loads; rows
 // past the batch or the vocabulary read zero and cost no traffic). LDS rows
 // are padded to 72 bf16 (144 bytes) so the 16-byte fragment reads of 32 rows
 // spread over the banks.
@@ -27,20 +27,30 @@ namespace nerve {
 namespace {
 
 constexpr int kLmThreads = 512;
-constexpr uint32_t kMt = 256, kNt = 128, kKt = 64, kRow = kKt + 8;  // LDS row: 72 bf16
+#ifndef NERVE_LM_KT
+#define NERVE_LM_KT 64
+#endif
+#ifndef NERVE_LM_WG_PER_CU
+#define NERVE_LM_WG_PER_CU 1
+#endif
+constexpr uint32_t kMt = 256, kNt = 128, kKt = NERVE_LM_KT, kRow = kKt + 8;  // LDS row: kKt + 8 bf16
 constexpr uint32_t kStageA = kMt * kRow, kStageW = kNt * kRow;      // bf16 per stage buffer
-constexpr uint32_t kLmLds = 2u * (kStageA + kStageW) * 2u;          // bytes: 110,592
+constexpr uint32_t kLmLds = 2u * (kStageA + kStageW) * 2u;          // bytes (110,592 with 64-column stages)
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4v;
 
+constexpr int kChunkA = (int)(kMt * kKt / 8u / kLmThreads);  // 16-byte chunks per thread and stage
+constexpr int kChunkW = (int)(kNt * kKt / 8u / kLmThreads);
+constexpr uint32_t kChunksPerRow = kKt / 8u;
 struct StageRegs {
-    u32x4v a[4];
-    u32x4v w[2];
+    u32x4v a[kChunkA];
+    u32x4v w[kChunkW];
 };
 
-__global__ __launch_bounds__(kLmThreads) void lm_head_kernel(const uint16_t *frames, uint64_t lda, const uint16_t *weight,
+template <int NS>
+__global__ __launch_bounds__(kLmThreads, NERVE_LM_WG_PER_CU) void lm_head_kernel(const uint16_t *frames, uint64_t lda, const uint16_t *weight,
                                                              uint64_t ldw, uint32_t B, uint32_t D, uint32_t V, float scale,
                                                              float *logits, uint64_t ldc, uint2 *records, uint32_t rec_stride) {
     extern __shared__ __align__(16) uint16_t s_lm[];
@@ -56,14 +66,14 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(const uint16_t *fra
     // valid ones are out of the resource's range (they read zero)
     auto issue = [&](StageRegs &r, uint32_t k0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t c = tid + (uint32_t)i * kLmThreads, row = c >> 3, col = k0 + (c & 7u) * 8u;
+        for (int i = 0; i < kChunkA; ++i) {
+            const uint32_t c = tid + (uint32_t)i * kLmThreads, row = c / kChunksPerRow, col = k0 + (c % kChunksPerRow) * 8u;
             const uint32_t off = row < mrows ? (uint32_t)(((uint64_t)row * lda + col) * 2u) : 0x7fffffffu;
             r.a[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t c = tid + (uint32_t)i * kLmThreads, row = c >> 3, col = k0 + (c & 7u) * 8u;
+        for (int i = 0; i < kChunkW; ++i) {
+            const uint32_t c = tid + (uint32_t)i * kLmThreads, row = c / kChunksPerRow, col = k0 + (c % kChunksPerRow) * 8u;
             const uint32_t off = row < nrows ? (uint32_t)(((uint64_t)row * ldw + col) * 2u) : 0x7fffffffu;
             r.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0);
         }
@@ -72,14 +82,14 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(const uint16_t *fra
         uint16_t *sa = s_lm + buf * (kStageA + kStageW);
         uint16_t *sw = sa + kStageA;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < kChunkA; ++i) {
             const uint32_t c = tid + (uint32_t)i * kLmThreads;
-            *(u32x4v *)(sa + (c >> 3) * kRow + (c & 7u) * 8u) = r.a[i];
+            *(u32x4v *)(sa + (c / kChunksPerRow) * kRow + (c % kChunksPerRow) * 8u) = r.a[i];
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < kChunkW; ++i) {
             const uint32_t c = tid + (uint32_t)i * kLmThreads;
-            *(u32x4v *)(sw + (c >> 3) * kRow + (c & 7u) * 8u) = r.w[i];
+            *(u32x4v *)(sw + (c / kChunksPerRow) * kRow + (c % kChunksPerRow) * 8u) = r.w[i];
         }
     };
     const uint32_t wm = wave & 3u, wn = wave >> 2;
@@ -94,7 +104,7 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(const uint16_t *fra
         const uint16_t *sa = s_lm + buf * (kStageA + kStageW);
         const uint16_t *sw = sa + kStageA;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
+        for (int ks = 0; ks < (int)(kKt / 16u); ++ks) {
             const uint32_t kk = (uint32_t)ks * 16u + 8u * (lane >> 5);
             bf16x8 af[2], bf[2];
 #pragma unroll
@@ -110,25 +120,42 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(const uint16_t *fra
         }
     };
 
-    const uint32_t S = D / kKt;  // D is a multiple of 64 (checked by the host)
-    StageRegs r0, r1;
-    issue(r0, 0u);
-    if (S > 1u) issue(r1, kKt);
-    store(r0, 0u);
+    const uint32_t S = D / kKt;  // D is a multiple of 64 (checked by the host), so of kKt
+    // A ring of NS register sets: stage s + 1 .. s + NS are in flight while
+    // stage s is computed from LDS buffer s & 1; set s % NS is free once
+    // stage s is in LDS, and takes stage s + NS.
+    auto kofs = [&](uint32_t st) __attribute__((always_inline)) -> uint32_t { return st * kKt; };
+    StageRegs R[NS];
+    static_for<0, NS>([&](auto Q) __attribute__((always_inline)) {
+        if ((uint32_t)Q < S) issue(R[Q], kofs((uint32_t)Q));
+    });
+    store(R[0], 0u);
     __syncthreads();
-    // stage s is in LDS buffer s & 1; the registers of stage s + 1 are in
-    // flight; stage s + 2 is issued into the set just stored
-    for (uint32_t s = 0; s < S; s += 2u) {
-        if (s + 2u < S) issue(r0, (s + 2u) * kKt);
-        compute(0u);
-        if (s + 1u < S) store(r1, 1u);
-        __syncthreads();
-        if (s + 1u >= S) break;
-        if (s + 3u < S) issue(r1, (s + 3u) * kKt);
-        compute(1u);
-        if (s + 2u < S) store(r0, 0u);
-        __syncthreads();
+    // Steady state, free of conditionals (so the compiler's wait counts
+    // follow each set exactly instead of waiting for every load in flight):
+    // NS steps per trip, each issuing stage s + NS.
+    uint32_t s0 = 0;
+    for (; s0 + 2u * NS <= S; s0 += NS) {
+        static_for<0, NS>([&](auto Q) __attribute__((always_inline)) {
+            constexpr int q = Q;
+            const uint32_t s = s0 + (uint32_t)q;
+            issue(R[q], kofs(s + NS));
+            compute(s & 1u);
+            store(R[(q + 1) % NS], (s + 1u) & 1u);
+            __syncthreads();
+        });
     }
+    // the last stages (fewer than 2 NS)
+    static_for<0, 2 * NS>([&](auto Q) __attribute__((always_inline)) {
+        constexpr int q = Q;
+        const uint32_t s = s0 + (uint32_t)q;
+        if (s < S) {
+            if (s + NS < S) issue(R[q % NS], kofs(s + NS));
+            compute(s & 1u);
+            if (s + 1u < S) store(R[(q + 1) % NS], (s + 1u) & 1u);
+            __syncthreads();
+        }
+    });
 
     // epilogue: scaled logits, and the tile record of each row's 64 columns
     if (!active) return;
@@ -160,6 +187,10 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(const uint16_t *fra
     }
 }
 
+#ifndef NERVE_LM_STAGES
+#define NERVE_LM_STAGES 3
+#endif
+constexpr int kLmStages = NERVE_LM_STAGES;  // register sets in the prefetch ring
 std::atomic<uint32_t> g_lds_set[kMaxDevices];
 
 }  // namespace
@@ -170,10 +201,10 @@ hipError_t launch_lm_head(const uint16_t *frames, uint64_t frames_ld, const uint
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    e = ensure_dyn_lds(lm_head_kernel, dev, kLmLds, g_lds_set);
+    e = ensure_dyn_lds(lm_head_kernel<kLmStages>, dev, kLmLds, g_lds_set);
     if (e != hipSuccess) return e;
     const dim3 grid((vocab + kNt - 1u) / kNt, (batch + kMt - 1u) / kMt);
-    hipLaunchKernelGGL(lm_head_kernel, grid, dim3(kLmThreads), kLmLds, stream, frames, frames_ld, weight, weight_ld, batch,
+    hipLaunchKernelGGL(lm_head_kernel<kLmStages>, grid, dim3(kLmThreads), kLmLds, stream, frames, frames_ld, weight, weight_ld, batch,
                        input_size, vocab, scale, logits, logits_ld, records, rec_stride);
     return hipGetLastError();
 }
