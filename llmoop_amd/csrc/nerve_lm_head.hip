@@ -26,33 +26,51 @@ namespace nerve {
 
 namespace {
 
-constexpr int kLmThreads = 512;
-#ifndef NERVE_LM_KT
-#define NERVE_LM_KT 64
-#endif
-#ifndef NERVE_LM_WG_PER_CU
-#define NERVE_LM_WG_PER_CU 1
-#endif
-constexpr uint32_t kMt = 256, kNt = 128, kKt = NERVE_LM_KT, kRow = kKt + 8;  // LDS row: kKt + 8 bf16
-constexpr uint32_t kStageA = kMt * kRow, kStageW = kNt * kRow;      // bf16 per stage buffer
-constexpr uint32_t kLmLds = 2u * (kStageA + kStageW) * 2u;          // bytes (110,592 with 64-column stages)
-
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4v;
 
-constexpr int kChunkA = (int)(kMt * kKt / 8u / kLmThreads);  // 16-byte chunks per thread and stage
-constexpr int kChunkW = (int)(kNt * kKt / 8u / kLmThreads);
-constexpr uint32_t kChunksPerRow = kKt / 8u;
-struct StageRegs {
-    u32x4v a[kChunkA];
-    u32x4v w[kChunkW];
+// Block shape: WM x WN waves, each owning TI x TJ MFMA tiles of 32 x 32, the
+// reduction staged KT columns at a time through double-buffered LDS, NS
+// register sets of loads in flight.
+template <int WM_, int WN_, int TI_, int TJ_, int KT_, int NS_, int WG_PER_CU_>
+struct LmCfg {
+    static constexpr int WM = WM_, WN = WN_, TI = TI_, TJ = TJ_, NS = NS_, WG_PER_CU = WG_PER_CU_;
+    static constexpr int kThreads = 64 * WM * WN;
+    static constexpr uint32_t kKt = KT_, kRow = KT_ + 8;  // LDS row: KT + 8 bf16 (spreads the 32 rows of a fragment read)
+    static constexpr uint32_t kMt = 32u * WM * TI, kNt = 32u * WN * TJ;
+    static constexpr uint32_t kStageA = kMt * kRow, kStageW = kNt * kRow;  // bf16 per stage buffer
+    static constexpr uint32_t kLds = 2u * (kStageA + kStageW) * 2u;        // bytes
+    static constexpr uint32_t kChunksPerRow = KT_ / 8u;
+    static constexpr int kChunkA = (int)(kMt * KT_ / 8u / kThreads);  // 16-byte chunks per thread and stage
+    static constexpr int kChunkW = (int)(kNt * KT_ / 8u / kThreads);
+    static_assert(kChunkA * kThreads * 8 == (int)(kMt * KT_) && kChunkW * kThreads * 8 == (int)(kNt * KT_), "chunks");
+    static_assert(TJ % 2 == 0, "a wave covers whole 64-column tiles");
 };
 
-template <int NS>
-__global__ __launch_bounds__(kLmThreads, NERVE_LM_WG_PER_CU) void lm_head_kernel(const uint16_t *frames, uint64_t lda, const uint16_t *weight,
-                                                             uint64_t ldw, uint32_t B, uint32_t D, uint32_t V, float scale,
-                                                             float *logits, uint64_t ldc, uint2 *records, uint32_t rec_stride) {
+// Maximum over each aligned group of 32 lanes: rotations by 1, 2, 4, 8 within
+// each row of 16 lanes (DPP row_ror, dpp_ctrl 0x121..0x128), then one swap of
+// the two rows of the group.
+__device__ __forceinline__ uint32_t max32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false));
+    return max(v, (uint32_t)__shfl_xor((int)v, 16, 64));
+}
+
+template <typename Cfg>
+__global__ __launch_bounds__(Cfg::kThreads, Cfg::WG_PER_CU) void lm_head_kernel(
+    const uint16_t *frames, uint64_t lda, const uint16_t *weight, uint64_t ldw, uint32_t B, uint32_t D, uint32_t V,
+    float scale, float *logits, uint64_t ldc, uint2 *records, uint32_t rec_stride) {
+    constexpr int NS = Cfg::NS, TI = Cfg::TI, TJ = Cfg::TJ;
+    constexpr int NT = Cfg::kThreads;
+    constexpr uint32_t kKt = Cfg::kKt, kRow = Cfg::kRow, kMt = Cfg::kMt, kNt = Cfg::kNt;
+    constexpr uint32_t kStageA = Cfg::kStageA, kStageW = Cfg::kStageW, kCpr = Cfg::kChunksPerRow;
+    struct StageRegs {
+        u32x4v a[Cfg::kChunkA];
+        u32x4v w[Cfg::kChunkW];
+    };
     extern __shared__ __align__(16) uint16_t s_lm[];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t n0 = blockIdx.x * kNt, m0 = blockIdx.y * kMt;
@@ -62,18 +80,18 @@ __global__ __launch_bounds__(kLmThreads, NERVE_LM_WG_PER_CU) void lm_head_kernel
         (void *)(frames + (uint64_t)m0 * lda), (short)0, (int)((uint64_t)(mrows - 1u) * lda * 2u + (uint64_t)D * 2u), 0x00020000);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(weight + (uint64_t)n0 * ldw), (short)0, (int)((uint64_t)(nrows - 1u) * ldw * 2u + (uint64_t)D * 2u), 0x00020000);
-    // chunk c of a stage: row c / 8, 16 bytes at column 8 (c % 8); rows past the
-    // valid ones are out of the resource's range (they read zero)
+    // chunk c of a stage: row c / kCpr, 16 bytes at column 8 (c % kCpr); rows
+    // past the valid ones are out of the resource's range (they read zero)
     auto issue = [&](StageRegs &r, uint32_t k0) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < kChunkA; ++i) {
-            const uint32_t c = tid + (uint32_t)i * kLmThreads, row = c / kChunksPerRow, col = k0 + (c % kChunksPerRow) * 8u;
+        for (int i = 0; i < Cfg::kChunkA; ++i) {
+            const uint32_t c = tid + (uint32_t)i * NT, row = c / kCpr, col = k0 + (c % kCpr) * 8u;
             const uint32_t off = row < mrows ? (uint32_t)(((uint64_t)row * lda + col) * 2u) : 0x7fffffffu;
             r.a[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < kChunkW; ++i) {
-            const uint32_t c = tid + (uint32_t)i * kLmThreads, row = c / kChunksPerRow, col = k0 + (c % kChunksPerRow) * 8u;
+        for (int i = 0; i < Cfg::kChunkW; ++i) {
+            const uint32_t c = tid + (uint32_t)i * NT, row = c / kCpr, col = k0 + (c % kCpr) * 8u;
             const uint32_t off = row < nrows ? (uint32_t)(((uint64_t)row * ldw + col) * 2u) : 0x7fffffffu;
             r.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0);
         }
@@ -82,23 +100,23 @@ __global__ __launch_bounds__(kLmThreads, NERVE_LM_WG_PER_CU) void lm_head_kernel
         uint16_t *sa = s_lm + buf * (kStageA + kStageW);
         uint16_t *sw = sa + kStageA;
 #pragma unroll
-        for (int i = 0; i < kChunkA; ++i) {
-            const uint32_t c = tid + (uint32_t)i * kLmThreads;
-            *(u32x4v *)(sa + (c / kChunksPerRow) * kRow + (c % kChunksPerRow) * 8u) = r.a[i];
+        for (int i = 0; i < Cfg::kChunkA; ++i) {
+            const uint32_t c = tid + (uint32_t)i * NT;
+            *(u32x4v *)(sa + (c / kCpr) * kRow + (c % kCpr) * 8u) = r.a[i];
         }
 #pragma unroll
-        for (int i = 0; i < kChunkW; ++i) {
-            const uint32_t c = tid + (uint32_t)i * kLmThreads;
-            *(u32x4v *)(sw + (c / kChunksPerRow) * kRow + (c % kChunksPerRow) * 8u) = r.w[i];
+        for (int i = 0; i < Cfg::kChunkW; ++i) {
+            const uint32_t c = tid + (uint32_t)i * NT;
+            *(u32x4v *)(sw + (c / kCpr) * kRow + (c % kCpr) * 8u) = r.w[i];
         }
     };
-    const uint32_t wm = wave & 3u, wn = wave >> 2;
-    const bool active = wm * 64u < mrows;  // waves past the batch only load and sync
-    f32x16 acc[2][2];
+    const uint32_t wm = wave % (uint32_t)Cfg::WM, wn = wave / (uint32_t)Cfg::WM;
+    const bool active = wm * 32u * TI < mrows;  // waves past the batch only load and sync
+    f32x16 acc[TI][TJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = (f32x16){};
+        for (int j = 0; j < TJ; ++j) acc[i][j] = (f32x16){};
     auto compute = [&](uint32_t buf) __attribute__((always_inline)) {
         if (!active) return;
         const uint16_t *sa = s_lm + buf * (kStageA + kStageW);
@@ -106,28 +124,27 @@ __global__ __launch_bounds__(kLmThreads, NERVE_LM_WG_PER_CU) void lm_head_kernel
 #pragma unroll
         for (int ks = 0; ks < (int)(kKt / 16u); ++ks) {
             const uint32_t kk = (uint32_t)ks * 16u + 8u * (lane >> 5);
-            bf16x8 af[2], bf[2];
+            bf16x8 af[TI], bf[TJ];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                af[i] = __builtin_bit_cast(bf16x8, *(const u32x4v *)(sa + (wm * 64u + (uint32_t)i * 32u + (lane & 31u)) * kRow + kk));
+            for (int i = 0; i < TI; ++i)
+                af[i] = __builtin_bit_cast(bf16x8, *(const u32x4v *)(sa + (wm * 32u * TI + (uint32_t)i * 32u + (lane & 31u)) * kRow + kk));
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                bf[j] = __builtin_bit_cast(bf16x8, *(const u32x4v *)(sw + (wn * 64u + (uint32_t)j * 32u + (lane & 31u)) * kRow + kk));
+            for (int j = 0; j < TJ; ++j)
+                bf[j] = __builtin_bit_cast(bf16x8, *(const u32x4v *)(sw + (wn * 32u * TJ + (uint32_t)j * 32u + (lane & 31u)) * kRow + kk));
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < TI; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < TJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
     };
 
     const uint32_t S = D / kKt;  // D is a multiple of 64 (checked by the host), so of kKt
-    // A ring of NS register sets: stage s + 1 .. s + NS are in flight while
+    // A ring of NS register sets: stages s + 1 .. s + NS are in flight while
     // stage s is computed from LDS buffer s & 1; set s % NS is free once
     // stage s is in LDS, and takes stage s + NS.
-    auto kofs = [&](uint32_t st) __attribute__((always_inline)) -> uint32_t { return st * kKt; };
     StageRegs R[NS];
     static_for<0, NS>([&](auto Q) __attribute__((always_inline)) {
-        if ((uint32_t)Q < S) issue(R[Q], kofs((uint32_t)Q));
+        if ((uint32_t)Q < S) issue(R[Q], (uint32_t)Q * kKt);
     });
     store(R[0], 0u);
     __syncthreads();
@@ -139,7 +156,7 @@ __global__ __launch_bounds__(kLmThreads, NERVE_LM_WG_PER_CU) void lm_head_kernel
         static_for<0, NS>([&](auto Q) __attribute__((always_inline)) {
             constexpr int q = Q;
             const uint32_t s = s0 + (uint32_t)q;
-            issue(R[q], kofs(s + NS));
+            issue(R[q], (s + NS) * kKt);
             compute(s & 1u);
             store(R[(q + 1) % NS], (s + 1u) & 1u);
             __syncthreads();
@@ -150,7 +167,7 @@ __global__ __launch_bounds__(kLmThreads, NERVE_LM_WG_PER_CU) void lm_head_kernel
         constexpr int q = Q;
         const uint32_t s = s0 + (uint32_t)q;
         if (s < S) {
-            if (s + NS < S) issue(R[q % NS], kofs(s + NS));
+            if (s + NS < S) issue(R[q % NS], (s + NS) * kKt);
             compute(s & 1u);
             if (s + 1u < S) store(R[(q + 1) % NS], (s + 1u) & 1u);
             __syncthreads();
@@ -158,39 +175,46 @@ __global__ __launch_bounds__(kLmThreads, NERVE_LM_WG_PER_CU) void lm_head_kernel
     });
 
     // epilogue: scaled logits, and the tile record of each row's 64 columns
+    // (columns 64 p .. 64 p + 63 of the wave are its MFMA tiles 2 p, 2 p + 1)
     if (!active) return;
-    const uint32_t tile = n0 / 64u + wn;
     const uint64_t half = lane < 32u ? 0x00000000ffffffffull : 0xffffffff00000000ull;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < TI; ++i) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const uint32_t m = m0 + wm * 64u + (uint32_t)i * 32u + 8u * (uint32_t)(r / 4) + 4u * (lane >> 5) + (uint32_t)(r % 4);
-            uint32_t key = 0u, nan = 0u;
-            uint64_t nb = 0u;
+            const uint32_t m = m0 + wm * 32u * TI + (uint32_t)i * 32u + 8u * (uint32_t)(r / 4) + 4u * (lane >> 5) + (uint32_t)(r % 4);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const uint32_t n = n0 + wn * 64u + (uint32_t)j * 32u + (lane & 31u);
-                const float v = acc[i][j][r] * scale;
-                const bool ok = m < B && n < V;
-                if (ok) logits[(uint64_t)m * ldc + n] = v;
-                const uint32_t bits = f2u(v);
-                key = max(key, ok ? raw_order_key(bits) : 0u);
-                nb = __ballot(ok && (bits & 0x7fffffffu) > 0x7f800000u);
-                nan += (uint32_t)__popcll(nb & half);
+            for (int p = 0; p < TJ / 2; ++p) {
+                uint32_t key = 0u, nan = 0u;
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const int j = 2 * p + jj;
+                    const uint32_t n = n0 + wn * 32u * TJ + (uint32_t)j * 32u + (lane & 31u);
+                    const float v = acc[i][j][r] * scale;
+                    const bool ok = m < B && n < V;
+                    if (ok) logits[(uint64_t)m * ldc + n] = v;
+                    const uint32_t bits = f2u(v);
+                    key = max(key, ok ? raw_order_key(bits) : 0u);
+                    nan += (uint32_t)__popcll(__ballot(ok && (bits & 0x7fffffffu) > 0x7f800000u) & half);
+                }
+                key = max32(key);
+                const uint32_t c0 = n0 + wn * 32u * TJ + 64u * (uint32_t)p;
+                if ((lane & 31u) == 0u && m < B && records && c0 < V)
+                    records[(uint64_t)m * rec_stride + c0 / 64u] = make_uint2(key, nan);
             }
-#pragma unroll
-            for (int o = 1; o < 32; o <<= 1) key = max(key, (uint32_t)__shfl_xor((int)key, o, 64));
-            if ((lane & 31u) == 0u && m < B && records && n0 + wn * 64u < V)
-                records[(uint64_t)m * rec_stride + tile] = make_uint2(key, nan);
         }
     }
 }
 
-#ifndef NERVE_LM_STAGES
-#define NERVE_LM_STAGES 3
-#endif
-constexpr int kLmStages = NERVE_LM_STAGES;  // register sets in the prefetch ring
+// 512 threads, 256 x 128 blocks, 64 x 64 per wave, 64-column stages, 3 sets of
+// loads in flight. Measured on MI355X at B=256, D=4096, V=151936 (gemm +
+// records, us): this shape 512; 256 x 256 blocks with 128 x 128 per wave
+// (4 waves, accumulators in AGPRs) 623; 256 x 256 with 64 x 128 per wave
+// 515-518; 2 / 4 / 5 sets in flight 518-544; two workgroups per CU with
+// 32-column stages 525; non-temporal weight loads, padded row strides and
+// rotated stage order within noise.
+using Lm = LmCfg<4, 2, 2, 2, 64, 3, 1>;
+
 std::atomic<uint32_t> g_lds_set[kMaxDevices];
 
 }  // namespace
@@ -201,10 +225,10 @@ hipError_t launch_lm_head(const uint16_t *frames, uint64_t frames_ld, const uint
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    e = ensure_dyn_lds(lm_head_kernel<kLmStages>, dev, kLmLds, g_lds_set);
+    e = ensure_dyn_lds(lm_head_kernel<Lm>, dev, Lm::kLds, g_lds_set);
     if (e != hipSuccess) return e;
-    const dim3 grid((vocab + kNt - 1u) / kNt, (batch + kMt - 1u) / kMt);
-    hipLaunchKernelGGL(lm_head_kernel<kLmStages>, grid, dim3(kLmThreads), kLmLds, stream, frames, frames_ld, weight, weight_ld, batch,
+    const dim3 grid((vocab + Lm::kNt - 1u) / Lm::kNt, (batch + Lm::kMt - 1u) / Lm::kMt);
+    hipLaunchKernelGGL(lm_head_kernel<Lm>, grid, dim3(Lm::kThreads), Lm::kLds, stream, frames, frames_ld, weight, weight_ld, batch,
                        input_size, vocab, scale, logits, logits_ld, records, rec_stride);
     return hipGetLastError();
 }

@@ -520,7 +520,7 @@ int nerve_lm_head_project(const void *frames, uint32_t frames_row_stride, const 
         return fail(NERVE_ERR_INVALID_ARGUMENT, "frames and weight must be 16-byte aligned");
     if (logits_row_stride < vocab_size) return fail(NERVE_ERR_INVALID_LOGITS_BYTE_CAPACITY, "logits_row_stride < vocab_size");
     if ((uint64_t)(batch < 256u ? batch : 256u) * frames_row_stride * 2u >= (1ull << 31) ||
-        (uint64_t)128u * weight_row_stride * 2u >= (1ull << 31))
+        (uint64_t)256u * weight_row_stride * 2u >= (1ull << 31))
         return fail(NERVE_ERR_INVALID_ARGUMENT, "row strides too large");
     const uint32_t ntiles = (vocab_size + nerve::tile_columns() - 1u) / nerve::tile_columns();
     if (tile_records && tile_stride < ntiles) return fail(NERVE_ERR_INVALID_ARGUMENT, "tile_stride < ceil(vocab/64)");
