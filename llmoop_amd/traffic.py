@@ -5,7 +5,8 @@ a kernel that reads and writes a known number of bytes, measured in the same
 rocprofv3 run, gives the factor that turns them into bytes.
 
   python llmoop_amd/traffic.py run --config C5 --steps 50 --calibrate-mib 256
-      runs `steps` sampling steps of the workload, then 20 elementwise
+      runs `steps` sampling steps of the workload (L5: projection with tile
+      records + tile step), then 20 elementwise
       negations of MIB MiB of float32 (each reads and writes exactly MIB MiB);
       meant to run under `rocprofv3 --pmc FETCH_SIZE` (then WRITE_SIZE)
   python llmoop_amd/traffic.py summary DIR [DIR ...] --calibrate-mib 256
@@ -31,14 +32,47 @@ KERNEL = "sample_rows_kernel"
 COPY_KERNEL = "neg_kernel"
 
 
-def run(config: str, steps: int, calibrate_mib: int) -> None:
+def run_l5(steps: int) -> None:
+    """The fused decode tail of L5: projection with tile records, then the tile step."""
     import torch
 
     from llmoop_amd import sampler as S
     from llmoop_amd import workloads
 
     dev = torch.device("cuda:0")
-    w = workloads.make(config, seed=2024, step=0)
+    w = workloads.make("L5", seed=2024, step=0)
+    frames, weight = workloads.lm_head_inputs(w, dev)
+    B, V = w.batch, w.vocab
+    smp = S.Sampler(V, B, dtype="f32", top_k_capacity=w.top_k_capacity, history_capacity=w.history.shape[1])
+    lg = torch.empty((B, V), dtype=torch.float32, device=dev)
+    rec = torch.empty((B, 2 * S.tile_count(V)), dtype=torch.int32, device=dev)
+
+    def dev_arr(a):
+        a = np.ascontiguousarray(a)
+        view = {np.uint32: np.int32, np.uint64: np.int64}.get(a.dtype.type, a.dtype.type)
+        return torch.from_numpy(a.view(view).copy()).to(dev)
+
+    params = S.params_tensor(w.params, dev)
+    kw = dict(history=dev_arr(w.history), history_len=dev_arr(w.history_len), seeds=dev_arr(w.seeds), rng=w.rng)
+    sc = torch.zeros((B, 5), dtype=torch.int32, device=dev)
+    out = torch.zeros((B, 4), dtype=torch.int32, device=dev)
+    for _ in range(steps):
+        S.lm_head_project(frames, weight, lg, output_scale=float(w.extra["scale"]), tile_records=rec)
+        smp.step(lg, params, out, stream_control=sc, tile_records=rec, **kw)
+    torch.cuda.synchronize()
+
+
+def run(config: str, steps: int, calibrate_mib: int) -> None:
+    import torch
+
+    from llmoop_amd import workloads
+
+    dev = torch.device("cuda:0")
+    if config.upper() == "L5":
+        run_l5(steps)
+        w = None
+    else:
+        w = workloads.make(config, seed=2024, step=0)
 
     def dev_arr(a):
         if a is None:
@@ -46,6 +80,22 @@ def run(config: str, steps: int, calibrate_mib: int) -> None:
         a = np.ascontiguousarray(a)
         view = {np.uint32: np.int32, np.uint16: np.int16, np.uint64: np.int64}.get(a.dtype.type, a.dtype.type)
         return torch.from_numpy(a.view(view).copy()).to(dev)
+
+    if w is not None:
+        _run_steps(w, steps, dev, dev_arr)
+    if calibrate_mib:
+        n = calibrate_mib * 2**20 // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+
+
+def _run_steps(w, steps, dev, dev_arr) -> None:
+    import torch
+
+    from llmoop_amd import sampler as S
 
     smp = S.Sampler(w.vocab, w.batch, dtype=w.dtype, top_k_capacity=w.top_k_capacity,
                     history_capacity=0 if w.history is None else w.history.shape[1])
@@ -57,13 +107,6 @@ def run(config: str, steps: int, calibrate_mib: int) -> None:
     for _ in range(steps):
         smp.step(lg, params, out, stream_control=sc, **kw)
     torch.cuda.synchronize()
-    if calibrate_mib:
-        n = calibrate_mib * 2**20 // 4
-        src = torch.ones(n, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(20):
-            torch.neg(src, out=dst)
-        torch.cuda.synchronize()
 
 
 def read_counters(directories) -> dict:
@@ -79,7 +122,7 @@ def read_counters(directories) -> dict:
     return {k: {c: list(v.values()) for c, v in d.items()} for k, d in out.items()}
 
 
-def summary(directories, calibrate_mib: int) -> int | None:
+def summary(directories, calibrate_mib: int, kernel: str = KERNEL) -> int | None:
     counters = read_counters(directories)
     rows = []
     for name, d in counters.items():
@@ -92,7 +135,7 @@ def summary(directories, calibrate_mib: int) -> int | None:
         vals = [m for name, c, m, _ in rows if c == counter and re.search(pattern, name)]
         return max(vals) if vals else None
 
-    fetch, write = pick(KERNEL, "FETCH_SIZE"), pick(KERNEL, "WRITE_SIZE")
+    fetch, write = pick(kernel, "FETCH_SIZE"), pick(kernel, "WRITE_SIZE")
     cfetch, cwrite = pick(COPY_KERNEL, "FETCH_SIZE"), pick(COPY_KERNEL, "WRITE_SIZE")
     if fetch is None or cfetch is None:
         print("missing sampling-kernel or calibration-kernel counters")
@@ -117,11 +160,12 @@ def main() -> None:
     s = sub.add_parser("summary")
     s.add_argument("dirs", nargs="+")
     s.add_argument("--calibrate-mib", type=int, default=256)
+    s.add_argument("--kernel", default=KERNEL, help="kernel name pattern of the per-launch traffic")
     a = ap.parse_args()
     if a.cmd == "run":
         run(a.config, a.steps, a.calibrate_mib)
     else:
-        summary(a.dirs, a.calibrate_mib)
+        summary(a.dirs, a.calibrate_mib, a.kernel)
 
 
 if __name__ == "__main__":
