@@ -113,8 +113,43 @@ def test_unaligned_row_stride_uses_scalar_loads(oracle):
     params = _random_params(rng, B, 32)
     _say("unaligned stride")
     ref = oracle.sample(x, params, top_k_capacity=32, vocab_size=V)
-    gpu = run_gpu(x, params, top_k_capacity=32, vocab=V)
+    from llmoop_amd import sampler as S
+
+    smp = S.Sampler(V, B, dtype="f32", top_k_capacity=32)
+    gpu = run_gpu(x, params, top_k_capacity=32, vocab=V, sampler=smp)
     assert_parity(gpu, ref, params, label="unaligned")
+    # the count the step used: one element per load, 512 x 16 tokens per slice
+    assert smp.slices_per_row == 1
+    smp.close()
+
+
+def test_large_vocab_with_kcap_1024(oracle):
+    """V = 201088 bf16 with top_k_capacity 1024: the handle is sized for the
+    16-byte-load kernels (2 slices per row, 3 by the automatic split of long
+    rows in short batches; the lists then exceed the in-kernel merge area and
+    the finish kernel merges them), and an unaligned row that would
+    need more slices than it holds is rejected with a message, not a fault."""
+    import torch
+
+    from llmoop_amd import sampler as S
+    from llmoop_amd.workloads import to_bf16_bits
+
+    rng = np.random.default_rng(8)
+    B, V = 4, 201088
+    x = to_bf16_bits((rng.standard_normal((B, V)) * 2).astype(np.float32))
+    params = _random_params(rng, B, 1024, method=1)
+    _say("V=201088 kcap=1024")
+    smp = S.Sampler(V, B, dtype="bf16", top_k_capacity=1024)
+    ref = oracle.sample(x, params, top_k_capacity=1024)
+    gpu = run_gpu(x, params, top_k_capacity=1024, sampler=smp)
+    assert_parity(gpu, ref, params, label="V=201088", prob_rtol=2e-3)
+    assert smp.slices_per_row == 3
+    dev = torch.device("cuda:0")
+    odd = torch.zeros((B, V + 1), dtype=torch.int16, device=dev)[:, 1:]  # 2-byte aligned rows only
+    out = torch.zeros((B, 4), dtype=torch.int32, device=dev)
+    with pytest.raises(S.SamplerError, match="slices"):
+        smp.step(odd, S.params_tensor(params, dev), out)
+    smp.close()
 
 
 def test_special_values(oracle):
