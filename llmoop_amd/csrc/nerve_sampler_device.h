@@ -940,6 +940,7 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
 }
 
 constexpr uint32_t kStageCap = 1024;       // lane-vectors staged for exact work per slice
+
 constexpr uint32_t kStreamCandCap = 2048;  // candidate entries per slice
 
 // Bytes of the staging area (lane-vectors and their slots).
@@ -1361,11 +1362,6 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
         else restage(std::false_type{});
         lds_sync();
         nstaged = sm.flag[2];
-    } else if (nstaged > 128u && nstaged > 2u * k) {
-        // a weak first-half threshold: refine it from every report before
-        // the exact pass (the staged set stays a superset)
-        const uint32_t t = report_threshold(1);
-        if (t > thr) set_thr(t);
     }
 
     // 5. exact keys of the staged elements (one lane per element), the tail,
