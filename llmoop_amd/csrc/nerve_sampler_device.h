@@ -380,11 +380,11 @@ struct RowCtx {
     bool history;
     const uint32_t *prefix;  // seen-state prefix of the row (set semantics), prefix_n ids
     uint32_t prefix_n;
+    bool whole_row;  // `bitmap` (from token 0) and `hash` cover every token of the row
 };
 
-template <typename Elem>
-__device__ __forceinline__ float configured_at(const RowCtx &c, uint32_t t) {
-    float x = load_elem<Elem>((const Elem *)c.logits_row, t);
+// The configured value of token t whose raw logit x the caller has loaded.
+__device__ __forceinline__ float configured_from(const RowCtx &c, uint32_t t, float x) {
     bool allowed = c.allowed_row ? ((c.allowed_row[t >> 5] >> (t & 31u)) & 1u) : true;
     uint32_t count = 0;
     if (c.history) {
@@ -403,6 +403,11 @@ __device__ __forceinline__ float configured_at(const RowCtx &c, uint32_t t) {
         for (uint32_t i = 0; i < c.prefix_n && count == 0u; ++i) count = c.prefix[i] == t ? 1u : 0u;
     }
     return configured_logit(x, allowed, count, c.rep, c.freq, c.pres);
+}
+
+template <typename Elem>
+__device__ __forceinline__ float configured_at(const RowCtx &c, uint32_t t) {
+    return configured_from(c, t, load_elem<Elem>((const Elem *)c.logits_row, t));
 }
 
 __device__ __forceinline__ bool float_better(float cl, uint32_t cid, float bl, uint32_t bid) {
@@ -721,32 +726,69 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
     } else if (!sampled) {
         if (row_flags & 2u) {
             // A NaN in the row: replay the reference lane structure exactly
-            // (greedy_sampler_f32:52-83), with penalties for the whole row.
-            if constexpr (PEN == 2) {
-                for (uint32_t i = tid; i < a.hash_slots; i += NT) s_hash[i] = kHashEmpty;
-                __syncthreads();
-                uint32_t len = a.history_len[row];
-                len = len > a.history_stride ? a.history_stride : len;
-                const uint32_t *hrow = a.history + (uint64_t)row * a.history_stride;
-                for (uint32_t i = tid; i < len; i += NT)
-                    if (hrow[i] < a.vocab) hash_insert(s_hash, a.log2_slots, hrow[i]);
+            // (greedy_sampler_f32:52-83), with penalties for the whole row:
+            // the caller's state when it covers the row (a bitmap probe per
+            // token, the table only for penalised ones), else the history's
+            // full counts rebuilt in the table.
+            RowCtx full = ctx;
+            if (!ctx.whole_row) {
+                if constexpr (PEN == 2) {
+                    for (uint32_t i = tid; i < a.hash_slots; i += NT) s_hash[i] = kHashEmpty;
+                    __syncthreads();
+                    uint32_t len = a.history_len[row];
+                    len = len > a.history_stride ? a.history_stride : len;
+                    const uint32_t *hrow = a.history + (uint64_t)row * a.history_stride;
+                    for (uint32_t i = tid; i < len; i += NT)
+                        if (hrow[i] < a.vocab) hash_insert(s_hash, a.log2_slots, hrow[i]);
+                }
+                full.bitmap = nullptr;
             }
             __syncthreads();
-            RowCtx full = ctx;
-            full.bitmap = nullptr;
             uint2 *slots = s_big;  // 1024 entries of (float bits, id)
-            for (uint32_t L = tid; L < 1024u; L += NT) {
-                uint32_t bid = L;
-                float best = L < a.vocab ? configured_at<Elem>(full, L) : u2f(kLowestBits);
-                for (uint32_t t = L + 1024u; t < a.vocab; t += 1024u) {
-                    const float c = configured_at<Elem>(full, t);
-                    if (float_better(c, t, best, bid)) {
-                        best = c;
-                        bid = t;
-                    }
-                }
-                slots[L] = make_uint2(f2u(best), bid);
+            // The thread's reference lanes L = tid + NT q advance together,
+            // 8 strides of each loaded before any is compared. A lane whose
+            // first value is NaN keeps it (no comparison with NaN succeeds);
+            // the others visit their values in order.
+            constexpr int Q = 1024 / NT;
+            float best[Q];
+            uint32_t bid[Q];
+#pragma unroll
+            for (int q = 0; q < Q; ++q) {
+                const uint32_t L = tid + (uint32_t)q * NT;
+                bid[q] = L;
+                best[q] = L < a.vocab ? configured_at<Elem>(full, L) : u2f(kLowestBits);
             }
+            for (uint32_t t0 = 1024u; t0 < a.vocab; t0 += 8u * 1024u) {
+                // raw values first (no control flow between the loads), then
+                // the penalties from registers
+                float c[Q][8];
+#pragma unroll
+                for (int q = 0; q < Q; ++q)
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const uint32_t t = t0 + tid + (uint32_t)q * NT + (uint32_t)u * 1024u;
+                        c[q][u] = load_elem<Elem>((const Elem *)full.logits_row, t < a.vocab ? t : 0u);
+                    }
+#pragma unroll
+                for (int q = 0; q < Q; ++q)
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const uint32_t t = t0 + tid + (uint32_t)q * NT + (uint32_t)u * 1024u;
+                        c[q][u] = t < a.vocab ? configured_from(full, t, c[q][u]) : u2f(kLowestBits);
+                    }
+#pragma unroll
+                for (int q = 0; q < Q; ++q)
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const uint32_t t = t0 + tid + (uint32_t)q * NT + (uint32_t)u * 1024u;
+                        if (t < a.vocab && float_better(c[q][u], t, best[q], bid[q])) {
+                            best[q] = c[q][u];
+                            bid[q] = t;
+                        }
+                    }
+            }
+#pragma unroll
+            for (int q = 0; q < Q; ++q) slots[tid + (uint32_t)q * NT] = make_uint2(f2u(best[q]), bid[q]);
             __syncthreads();
             for (uint32_t stride = 512u; stride > 0u; stride >>= 1) {
                 for (uint32_t L = tid; L < stride; L += NT) {
@@ -1608,6 +1650,7 @@ __global__ __launch_bounds__(kBlock) void sample_rows_kernel(StepArgs a) {
     ctx.history = history;
     ctx.prefix = PEN == 1 && a.prefix_ids ? a.prefix_ids + (uint64_t)row * a.prefix_stride : nullptr;
     ctx.prefix_n = PEN == 1 ? prefix_count(a, row) : 0u;
+    ctx.whole_row = a.slices == 1u && PEN != 0;  // one slice: its bitmap (from token 0) and table are the row's
 
     // 7. selection -> s_sorted[0 .. n_out)
     uint32_t C = sm.flag[1];
@@ -1908,6 +1951,7 @@ __device__ __forceinline__ RowCtx row_ctx(const StepArgs &a, uint32_t row, const
     ctx.history = PEN == 2;
     ctx.prefix = PEN == 1 && a.prefix_ids ? a.prefix_ids + (uint64_t)row * a.prefix_stride : nullptr;
     ctx.prefix_n = PEN == 1 ? prefix_count(a, row) : 0u;
+    ctx.whole_row = false;
     return ctx;
 }
 

@@ -381,6 +381,7 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
     ctx.history = PEN == 2;
     ctx.prefix = nullptr;
     ctx.prefix_n = 0u;
+    ctx.whole_row = PEN != 0;  // the bitmap covers the row (prefix included), the table holds its repeats
     // rank sort: 4 adjacent lanes per candidate, each counting the better
     // entries among every 4th one (8 reads in flight), the counts summed
     // across the 4 lanes (ids are distinct, so ranks are a permutation)
@@ -414,14 +415,7 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
         if ((row_flags_in & 4u) || (PEN != 0 && !(pq - pq == 0.0f))) row_flags |= 2u;
     }
     const float u = sampled ? random_unit(a.rng, io.seed, (uint64_t)io.tick_lo | ((uint64_t)io.tick_hi << 32), row) : 0.0f;
-    // the finish's NaN replay recomputes configured values over the whole row
-    RowCtx fctx = ctx;
-    fctx.bitmap = nullptr;  // the replay rebuilds the table with full counts (history)
-    if constexpr (PEN == 1) {
-        fctx.prefix = a.prefix_ids ? a.prefix_ids + (uint64_t)row * a.prefix_stride : nullptr;
-        fctx.prefix_n = prefix_count(a, row);
-    }
-    finish_row<Elem, PEN, kBlock>(a, row, io, P, k, sampled, n, row_flags, s_sorted, s_big, s_w, s_p, s_hash, fctx, u);
+    finish_row<Elem, PEN, kBlock>(a, row, io, P, k, sampled, n, row_flags, s_sorted, s_big, s_w, s_p, s_hash, ctx, u);
 }
 
 template <typename Elem, int PEN, bool MASK>
