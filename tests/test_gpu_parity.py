@@ -106,6 +106,23 @@ def test_slice_count_does_not_change_results(oracle, slices):
     assert_parity(gpu, ref, params, label=f"slices={slices}")
 
 
+@pytest.mark.parametrize("slices", [1, 3])
+def test_greedy_nan_replay_with_history(oracle, slices):
+    """Greedy rows holding a NaN replay the reference lane structure with the
+    penalties: from the step's own bitmap and repeat table (one slice), or
+    from the history's counts rebuilt after the merge (several slices)."""
+    logits, params, kw = _make_case(91, 8, 40000, "f32", 64, "history", False, "normal")
+    params["method"] = 0
+    params["repetition_penalty"] = 1.3
+    logits[1, 700] = np.nan
+    logits[5, 39999] = np.nan
+    logits[6, 3] = np.nan  # in the first stride of the replay's lanes
+    _say(f"greedy nan replay slices={slices}")
+    ref = oracle.sample(logits, params, top_k_capacity=64, **kw)
+    gpu = run_gpu(logits, params, top_k_capacity=64, slices_per_row=slices, **kw)
+    assert_parity(gpu, ref, params, label=f"greedy-nan-{slices}")
+
+
 def test_unaligned_row_stride_uses_scalar_loads(oracle):
     rng = np.random.default_rng(5)
     B, V, stride = 6, 5001, 5003
