@@ -48,15 +48,16 @@ struct LmCfg {
     static_assert(TJ % 2 == 0, "a wave covers whole 64-column tiles");
 };
 
-// Maximum over each aligned group of 32 lanes: rotations by 1, 2, 4, 8 within
-// each row of 16 lanes (DPP row_ror, dpp_ctrl 0x121..0x128), then one swap of
-// the two rows of the group.
-__device__ __forceinline__ uint32_t max32(uint32_t v) {
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x121, 0xf, 0xf, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x122, 0xf, 0xf, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, false));
-    return max(v, (uint32_t)__shfl_xor((int)v, 16, 64));
+// Float maximum over each aligned group of 32 lanes, NaN ignored (fmaxf
+// returns the other operand): rotations by 1, 2, 4, 8 within each row of 16
+// lanes (DPP row_ror, dpp_ctrl 0x121..0x128), then one swap of the two rows
+// of the group.
+__device__ __forceinline__ float fmax32(float v) {
+    v = fmaxf(v, u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(v), 0x121, 0xf, 0xf, false)));
+    v = fmaxf(v, u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(v), 0x122, 0xf, 0xf, false)));
+    v = fmaxf(v, u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(v), 0x124, 0xf, 0xf, false)));
+    v = fmaxf(v, u2f((uint32_t)__builtin_amdgcn_update_dpp(0, (int)f2u(v), 0x128, 0xf, 0xf, false)));
+    return fmaxf(v, u2f((uint32_t)__shfl_xor((int)f2u(v), 16, 64)));
 }
 
 template <typename Cfg>
@@ -185,7 +186,11 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::WG_PER_CU) void lm_head_kernel(
             const uint32_t m = m0 + wm * 32u * TI + (uint32_t)i * 32u + 8u * (uint32_t)(r / 4) + 4u * (lane >> 5) + (uint32_t)(r % 4);
 #pragma unroll
             for (int p = 0; p < TJ / 2; ++p) {
-                uint32_t key = 0u, nan = 0u;
+                // the largest value as a float (NaN and columns past the
+                // vocabulary do not count), turned into its order key once;
+                // +0 and -0 share a key, so fmaxf's choice between them is moot
+                float mx = __builtin_nanf("");
+                uint32_t nan = 0u;
 #pragma unroll
                 for (int jj = 0; jj < 2; ++jj) {
                     const int j = 2 * p + jj;
@@ -193,11 +198,10 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::WG_PER_CU) void lm_head_kernel(
                     const float v = acc[i][j][r] * scale;
                     const bool ok = m < B && n < V;
                     if (ok) logits[(uint64_t)m * ldc + n] = v;
-                    const uint32_t bits = f2u(v);
-                    key = max(key, ok ? raw_order_key(bits) : 0u);
-                    nan += (uint32_t)__popcll(__ballot(ok && (bits & 0x7fffffffu) > 0x7f800000u) & half);
+                    mx = fmaxf(mx, ok ? v : __builtin_nanf(""));
+                    nan += (uint32_t)__popcll(__ballot(ok && v != v) & half);
                 }
-                key = max32(key);
+                const uint32_t key = raw_order_key(f2u(fmax32(mx)));
                 const uint32_t c0 = n0 + wn * 32u * TJ + 64u * (uint32_t)p;
                 if ((lane & 31u) == 0u && m < B && records && c0 < V)
                     records[(uint64_t)m * rec_stride + c0 / 64u] = make_uint2(key, nan);
