@@ -281,17 +281,36 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
                     ids[u] = e < nel ? s_ct[e / kTileCols] * kTileCols + (e % kTileCols) : 0xffffffffu;
                     bits[u] = ids[u] < V ? f2u(load_elem<Elem>(lrow, ids[u])) : 0u;
                 }
+                // keys of the round in registers (0: not a candidate), then
+                // one LDS atomic per wave for the round's appends
+                uint32_t keys[16];
+                uint32_t cnt = 0u;
 #pragma unroll
                 for (int u = 0; u < 16; ++u) {
                     const uint32_t id = ids[u];
-                    if (id >= V) continue;
-                    const uint32_t raw = raw_order_key(bits[u]);
-                    if (raw < thr) continue;  // configured <= raw for lowering penalties and masks
-                    if constexpr (PEN != 0) {
-                        if (!lowering && ((s_pen[id >> 5] >> (id & 31u)) & 1u)) continue;  // the penalised pass below
+                    uint32_t key = 0u;
+                    // configured <= raw for lowering penalties and masks
+                    if (id < V && raw_order_key(bits[u]) >= thr) {
+                        bool skip = false;
+                        if constexpr (PEN != 0) skip = !lowering && ((s_pen[id >> 5] >> (id & 31u)) & 1u);  // the penalised pass below
+                        if (!skip) key = key_of(id, bits[u]);
                     }
-                    const uint32_t key = key_of(id, bits[u]);
-                    if (key >= thr && key != 0u) push(key, id);
+                    keys[u] = key >= thr ? key : 0u;
+                    cnt += keys[u] != 0u ? 1u : 0u;
+                }
+                const uint32_t incl = wave_inclusive_scan(cnt);
+                const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
+                if (total) {
+                    uint32_t pos0 = 0u;
+                    if (lane == 63u) pos0 = atomicAdd(&sm.flag[1], total);
+                    uint32_t q = (uint32_t)__builtin_amdgcn_readlane((int)pos0, 63) + incl - cnt;
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) {
+                        if (keys[u] != 0u) {
+                            if (q < kStreamCandCap) s_cand[q] = cand_pack(keys[u], ids[u]);
+                            ++q;
+                        }
+                    }
                 }
             }
             if constexpr (PEN != 0) {
