@@ -6,14 +6,16 @@
 // columns, the tile record the sampling step reads: the largest order key of
 // the 64 logits and the count of NaNs among them.
 //
-// A workgroup of 8 waves computes a 256 x 128 (batch x vocabulary) block with
-// v_mfma_f32_32x32x16_bf16: wave w owns the 64 x 64 sub-block (w % 4, w / 4),
-// 2 x 2 MFMA tiles of 32 x 32 (64 accumulators per lane). The reduction
-// dimension goes through LDS 64 columns at a time, double-buffered, with the
-// global loads of a stage issued several stages ahead (16-byte buffer loads; rows
-// past the batch or the vocabulary read zero and cost no traffic). LDS rows
-// are padded to 72 bf16 (144 bytes) so the 16-byte fragment reads of 32 rows
-// spread over the banks.
+// A workgroup of 16 waves computes a 256 x 256 (batch x vocabulary) block
+// with v_mfma_f32_32x32x16_bf16: wave w owns the 64 x 64 sub-block
+// (w % 4, w / 4), 2 x 2 MFMA tiles of 32 x 32 (64 accumulators per lane). The
+// reduction dimension goes through LDS 64 columns at a time, double-buffered,
+// with the global loads of the next stage issued before the current one is
+// computed (16-byte buffer loads; rows past the batch or the vocabulary read
+// zero and cost no traffic). LDS rows are padded to 72 bf16 (144 bytes) so
+// the 16-byte fragment reads of 32 rows spread over the banks. The block
+// shape is a template parameter (LmCfg); the alternatives measured are listed
+// where the shape is chosen.
 //
 // MFMA operand layout (v_mfma_f32_32x32x16_bf16, checked on the GPU): lane l
 // supplies A[l % 32][8 (l / 32) .. + 8] and B[8 (l / 32) .. + 8][l % 32];
@@ -210,14 +212,17 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::WG_PER_CU) void lm_head_kernel(
     }
 }
 
-// 512 threads, 256 x 128 blocks, 64 x 64 per wave, 64-column stages, 3 sets of
-// loads in flight. Measured on MI355X at B=256, D=4096, V=151936 (gemm +
-// records, us): this shape 512; 256 x 256 blocks with 128 x 128 per wave
-// (4 waves, accumulators in AGPRs) 623; 256 x 256 with 64 x 128 per wave
-// 515-518; 2 / 4 / 5 sets in flight 518-544; two workgroups per CU with
-// 32-column stages 525; non-temporal weight loads, padded row strides and
-// rotated stage order within noise.
-using Lm = LmCfg<4, 2, 2, 2, 64, 3, 1>;
+// 1024 threads (16 waves), 256 x 256 blocks, 64 x 64 per wave, 64-column
+// stages, one set of loads in flight (128 VGPRs: four waves per SIMD). The
+// frames are read once per 256 vocabulary rows instead of once per 128.
+// Measured on MI355X at B=256, D=4096, V=151936 (gemm + records, us, same
+// session): this shape 491 against 527 for 8 waves in 256 x 128 blocks with
+// 3 sets in flight. Also measured with 8 waves: 256 x 256 blocks with
+// 128 x 128 per wave (4 waves, accumulators in AGPRs) 623; 256 x 256 with
+// 64 x 128 per wave 515-518; 2 / 4 / 5 sets in flight 518-544; two
+// workgroups per CU with 32-column stages 525; non-temporal weight loads,
+// padded row strides and rotated stage order within noise.
+using Lm = LmCfg<4, 4, 2, 2, 64, 1, 1>;
 
 std::atomic<uint32_t> g_lds_set[kMaxDevices];
 
