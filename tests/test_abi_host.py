@@ -144,3 +144,37 @@ def test_create_without_gpu_fails_cleanly(S):
     with pytest.raises(S.SamplerError) as e:
         S.Sampler(1000, 4)
     assert e.value.code in (S.ERR_HIP, S.ERR_INVALID_ARGUMENT)
+
+
+def test_fused_entry_points_reject_bad_arguments(S):
+    """The LM-head projection, the tile records and the tile step check their
+    arguments before any device call (placeholder pointers are never touched)."""
+    lib = S.load_library()
+    P = 0x1000  # 16-byte aligned placeholder
+    bad = [
+        # input_size not a multiple of 64
+        lambda: lib.nerve_lm_head_project(P, 100, P, 100, 4, 100, 1000, 1.0, P, 1000, None, 0, None),
+        # stride below input_size
+        lambda: lib.nerve_lm_head_project(P, 32, P, 64, 4, 64, 1000, 1.0, P, 1000, None, 0, None),
+        # misaligned frames
+        lambda: lib.nerve_lm_head_project(P + 2, 64, P, 64, 4, 64, 1000, 1.0, P, 1000, None, 0, None),
+        # logits stride below the vocabulary
+        lambda: lib.nerve_lm_head_project(P, 64, P, 64, 4, 64, 1000, 1.0, P, 999, None, 0, None),
+        # tile stride below ceil(V/64)
+        lambda: lib.nerve_lm_head_project(P, 64, P, 64, 4, 64, 1000, 1.0, P, 1000, P, 15, None),
+        # non-finite scale
+        lambda: lib.nerve_lm_head_project(P, 64, P, 64, 4, 64, 1000, float("inf"), P, 1000, None, 0, None),
+        # tile records: unknown dtype, short stride, misaligned records
+        lambda: lib.nerve_tile_records(P, 7, 1000, 4, 1000, P, 16, None),
+        lambda: lib.nerve_tile_records(P, 0, 1000, 4, 1000, P, 15, None),
+        lambda: lib.nerve_tile_records(P, 0, 1000, 4, 1000, P + 4, 16, None),
+        # tile step without records
+        lambda: lib.nerve_sampler_step_tiles(P, P, None, 16, None),
+    ]
+    for i, call in enumerate(bad):
+        rc = call()
+        assert rc != S.NERVE_OK, f"case {i} accepted"
+        assert lib.nerve_sampler_last_error(), f"case {i} left no message"
+    # nothing to do: empty batches succeed without touching the device
+    assert lib.nerve_lm_head_project(None, 0, None, 0, 0, 64, 1000, 1.0, None, 0, None, 0, None) == S.NERVE_OK
+    assert lib.nerve_tile_records(None, 0, 0, 0, 1000, None, 0, None) == S.NERVE_OK
