@@ -65,7 +65,8 @@ __device__ __forceinline__ float fmax32(float v) {
 template <typename Cfg>
 __global__ __launch_bounds__(Cfg::kThreads, Cfg::WG_PER_CU) void lm_head_kernel(
     const uint16_t *frames, uint64_t lda, const uint16_t *weight, uint64_t ldw, uint32_t B, uint32_t D, uint32_t V,
-    float scale, float *logits, uint64_t ldc, uint2 *records, uint32_t rec_stride) {
+    float scale, float *logits, uint64_t ldc, uint2 *records, uint32_t rec_stride, uint32_t full_blocks,
+    uint32_t tail_width) {
     constexpr int NS = Cfg::NS, TI = Cfg::TI, TJ = Cfg::TJ;
     constexpr int NT = Cfg::kThreads;
     constexpr uint32_t kKt = Cfg::kKt, kRow = Cfg::kRow, kMt = Cfg::kMt, kNt = Cfg::kNt;
@@ -76,9 +77,15 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::WG_PER_CU) void lm_head_kernel(
     };
     extern __shared__ __align__(16) uint16_t s_lm[];
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t n0 = blockIdx.x * kNt, m0 = blockIdx.y * kMt;
+    // the first full_blocks blocks are kNt columns wide; the rest (the last,
+    // partial round of the grid) tail_width, so that round spreads over more CUs
+    const uint32_t bx = blockIdx.x;
+    const uint32_t n0 = bx < full_blocks ? bx * kNt : full_blocks * kNt + (bx - full_blocks) * tail_width;
+    const uint32_t width = bx < full_blocks ? kNt : tail_width;
+    const uint32_t m0 = blockIdx.y * kMt;
     const uint32_t mrows = B - m0 < kMt ? B - m0 : kMt;
-    const uint32_t nrows = V - n0 < kNt ? V - n0 : kNt;
+    const uint32_t nrows = V - n0 < width ? V - n0 : width;
+    const uint32_t nend = n0 + nrows;  // columns of this block: [n0, nend)
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(frames + (uint64_t)m0 * lda), (short)0, (int)((uint64_t)(mrows - 1u) * lda * 2u + (uint64_t)D * 2u), 0x00020000);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
@@ -114,7 +121,7 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::WG_PER_CU) void lm_head_kernel(
         }
     };
     const uint32_t wm = wave % (uint32_t)Cfg::WM, wn = wave / (uint32_t)Cfg::WM;
-    const bool active = wm * 32u * TI < mrows;  // waves past the batch only load and sync
+    const bool active = wm * 32u * TI < mrows && wn * 32u * TJ < nrows;  // others only load and sync
     f32x16 acc[TI][TJ];
 #pragma unroll
     for (int i = 0; i < TI; ++i)
@@ -198,14 +205,14 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::WG_PER_CU) void lm_head_kernel(
                     const int j = 2 * p + jj;
                     const uint32_t n = n0 + wn * 32u * TJ + (uint32_t)j * 32u + (lane & 31u);
                     const float v = acc[i][j][r] * scale;
-                    const bool ok = m < B && n < V;
+                    const bool ok = m < B && n < nend;
                     if (ok) logits[(uint64_t)m * ldc + n] = v;
                     mx = fmaxf(mx, ok ? v : __builtin_nanf(""));
                     nan += (uint32_t)__popcll(__ballot(ok && v != v) & half);
                 }
                 const uint32_t key = raw_order_key(f2u(fmax32(mx)));
                 const uint32_t c0 = n0 + wn * 32u * TJ + 64u * (uint32_t)p;
-                if ((lane & 31u) == 0u && m < B && records && c0 < V)
+                if ((lane & 31u) == 0u && m < B && records && c0 < nend)
                     records[(uint64_t)m * rec_stride + c0 / 64u] = make_uint2(key, nan);
             }
         }
@@ -236,9 +243,28 @@ hipError_t launch_lm_head(const uint16_t *frames, uint64_t frames_ld, const uint
     if (e != hipSuccess) return e;
     e = ensure_dyn_lds(lm_head_kernel<Lm>, dev, Lm::kLds, g_lds_set);
     if (e != hipSuccess) return e;
-    const dim3 grid((vocab + Lm::kNt - 1u) / Lm::kNt, (batch + Lm::kMt - 1u) / Lm::kMt);
+    // Blocks of kNt columns fill whole rounds of the CUs (one block per CU);
+    // the columns left for a last, partial round go to blocks of kNt / 2, so
+    // that round takes about half as long.
+    static std::atomic<int> cu_count[kMaxDevices];
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    int cus = cu_count[dev].load(std::memory_order_relaxed);
+    if (cus == 0) {
+        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        cu_count[dev].store(cus, std::memory_order_relaxed);
+    }
+    const uint32_t blocks = (vocab + Lm::kNt - 1u) / Lm::kNt;
+    uint32_t full = blocks, tail_width = Lm::kNt, tail = 0u;
+    const uint32_t rounds = blocks / (uint32_t)cus;
+    if (rounds > 0u && blocks % (uint32_t)cus != 0u) {
+        full = rounds * (uint32_t)cus;
+        tail_width = Lm::kNt / 2u;
+        tail = (vocab - full * Lm::kNt + tail_width - 1u) / tail_width;
+    }
+    const dim3 grid(full + tail, (batch + Lm::kMt - 1u) / Lm::kMt);
     hipLaunchKernelGGL(lm_head_kernel<Lm>, grid, dim3(Lm::kThreads), Lm::kLds, stream, frames, frames_ld, weight, weight_ld, batch,
-                       input_size, vocab, scale, logits, logits_ld, records, rec_stride);
+                       input_size, vocab, scale, logits, logits_ld, records, rec_stride, full, tail_width);
     return hipGetLastError();
 }
 

@@ -59,7 +59,10 @@ def bf16_value(bits):
     return (bits.astype(np.uint32) << 16).view(np.float32)
 
 
-@pytest.mark.parametrize("B,D,V", [(1, 64, 1000), (37, 512, 4099), (256, 256, 8192), (300, 128, 1031)])
+# 70000 and 140000 columns need more 256-column blocks than the GPU has CUs:
+# the last, partial round uses 128-column blocks
+@pytest.mark.parametrize("B,D,V", [(1, 64, 1000), (37, 512, 4099), (256, 256, 8192), (300, 128, 1031),
+                                   (40, 64, 70000), (9, 128, 140000)])
 def test_lm_head_projection(B, D, V):
     import torch
 
