@@ -228,7 +228,10 @@ __global__ __launch_bounds__(Cfg::kThreads, Cfg::WG_PER_CU) void lm_head_kernel(
 // 128 x 128 per wave (4 waves, accumulators in AGPRs) 623; 256 x 256 with
 // 64 x 128 per wave 515-518; 2 / 4 / 5 sets in flight 518-544; two
 // workgroups per CU with 32-column stages 525; non-temporal weight loads,
-// padded row strides and rotated stage order within noise.
+// padded row strides and rotated stage order within noise. Loading the
+// stages straight into LDS (buffer loads with the LDS bit, 32-column stages,
+// 3 or 4 stages in flight in 4 or 5 LDS buffers, swizzled rows): 527-535
+// against 472-485 for this shape in the same session.
 using Lm = LmCfg<4, 4, 2, 2, 64, 1, 1>;
 
 std::atomic<uint32_t> g_lds_set[kMaxDevices];
