@@ -981,6 +981,15 @@ __device__ __forceinline__ void finish_row(const StepArgs &a, uint32_t row, cons
     }
 }
 
+// Defined after the slice kernel, which uses them for the last slice of a row.
+template <int NT, typename LoadEntry, typename LoadMeta>
+__device__ __forceinline__ uint32_t merge_slices(const StepArgs &a, uint32_t k, uint2 *s_big, uint2 *s_sorted,
+                                                 uint32_t *s_meta, uint32_t &row_flags, LoadEntry load_entry,
+                                                 LoadMeta load_meta);
+template <typename Elem, int PEN>
+__device__ __forceinline__ RowCtx row_ctx(const StepArgs &a, uint32_t row, const nerve_sampler_row_params &P,
+                                          uint32_t *s_hash);
+
 constexpr uint32_t kStageCap = 1024;       // lane-vectors staged for exact work per slice
 
 constexpr uint32_t kStreamCandCap = 2048;  // candidate entries per slice
