@@ -281,36 +281,56 @@ __global__ __launch_bounds__(kBlock) void sample_tiles_kernel(StepArgs a) {
                     ids[u] = e < nel ? s_ct[e / kTileCols] * kTileCols + (e % kTileCols) : 0xffffffffu;
                     bits[u] = ids[u] < V ? f2u(load_elem<Elem>(lrow, ids[u])) : 0u;
                 }
-                // keys of the round in registers (0: not a candidate), then
-                // one LDS atomic per wave for the round's appends
-                uint32_t keys[16];
-                uint32_t cnt = 0u;
+                // The raw test first (configured <= raw for lowering
+                // penalties and masks); a lane's first two passing elements
+                // go to two register slots, so the configured key (penalty
+                // lookup, division) runs twice per lane, not 16 times; a lane
+                // with more in the round (rare) computes the rest in place.
+                uint32_t cm = 0u;
 #pragma unroll
                 for (int u = 0; u < 16; ++u) {
                     const uint32_t id = ids[u];
-                    uint32_t key = 0u;
-                    // configured <= raw for lowering penalties and masks
-                    if (id < V && raw_order_key(bits[u]) >= thr) {
-                        bool skip = false;
-                        if constexpr (PEN != 0) skip = !lowering && ((s_pen[id >> 5] >> (id & 31u)) & 1u);  // the penalised pass below
-                        if (!skip) key = key_of(id, bits[u]);
-                    }
-                    keys[u] = key >= thr ? key : 0u;
-                    cnt += keys[u] != 0u ? 1u : 0u;
+                    bool c = id < V && raw_order_key(bits[u]) >= thr;
+                    if constexpr (PEN != 0) c = c && !(!lowering && ((s_pen[id >> 5] >> (id & 31u)) & 1u));  // the penalised pass below
+                    cm |= c ? (1u << u) : 0u;
                 }
+                uint32_t id0 = 0u, b0 = 0u, id1 = 0u, b1 = 0u;
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    const uint32_t before = (uint32_t)__builtin_popcount(cm & ((1u << u) - 1u));
+                    const bool c = (cm >> u) & 1u;
+                    id0 = c && before == 0u ? ids[u] : id0;
+                    b0 = c && before == 0u ? bits[u] : b0;
+                    id1 = c && before == 1u ? ids[u] : id1;
+                    b1 = c && before == 1u ? bits[u] : b1;
+                }
+                const uint32_t nc = (uint32_t)__builtin_popcount(cm);
+                uint32_t k0 = nc > 0u ? key_of(id0, b0) : 0u;
+                uint32_t k1 = nc > 1u ? key_of(id1, b1) : 0u;
+                k0 = k0 >= thr ? k0 : 0u;
+                k1 = k1 >= thr ? k1 : 0u;
+                if (nc > 2u) {
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) {
+                        if (((cm >> u) & 1u) && __builtin_popcount(cm & ((1u << u) - 1u)) >= 2) {
+                            const uint32_t key = key_of(ids[u], bits[u]);
+                            if (key >= thr && key != 0u) push(key, ids[u]);
+                        }
+                    }
+                }
+                // one LDS atomic per wave for the slots' appends
+                const uint32_t cnt = (k0 != 0u ? 1u : 0u) + (k1 != 0u ? 1u : 0u);
                 const uint32_t incl = wave_inclusive_scan(cnt);
                 const uint32_t total = (uint32_t)__builtin_amdgcn_readlane((int)incl, 63);
                 if (total) {
                     uint32_t pos0 = 0u;
                     if (lane == 63u) pos0 = atomicAdd(&sm.flag[1], total);
                     uint32_t q = (uint32_t)__builtin_amdgcn_readlane((int)pos0, 63) + incl - cnt;
-#pragma unroll
-                    for (int u = 0; u < 16; ++u) {
-                        if (keys[u] != 0u) {
-                            if (q < kStreamCandCap) s_cand[q] = cand_pack(keys[u], ids[u]);
-                            ++q;
-                        }
+                    if (k0 != 0u) {
+                        if (q < kStreamCandCap) s_cand[q] = cand_pack(k0, id0);
+                        ++q;
                     }
+                    if (k1 != 0u && q < kStreamCandCap) s_cand[q] = cand_pack(k1, id1);
                 }
             }
             if constexpr (PEN != 0) {
