@@ -22,6 +22,11 @@ After the timed steps the last one is recomputed with the CPU oracle at the
 same tick (same logits, history, seeds, Philox stream) and the bench fails on
 any mismatch, so the path timed is the path checked. HBM traffic counters are
 collected separately (llmoop_amd/traffic.py).
+
+--config L5 times the decode tail instead: the LM-head projection (bf16
+frames x bf16 tied weight -> f32 logits, with the tile-record epilogue) and the
+step over the tile records, next to the projection followed by the dense step
+and each kernel alone; the last fused step is checked against the oracle.
 """
 from __future__ import annotations
 
